@@ -1,0 +1,190 @@
+/*
+ * specfit_amd.h -- C ABI of the MI355X (gfx950) offloaded Qwen3-MoE
+ * verification path.
+ *
+ * Every entry point is enqueue-only: it validates its arguments on the host,
+ * launches HIP work on the caller's stream and returns.  Nothing here
+ * allocates device memory, synchronises the host, or keeps mutable global
+ * state; all buffers are owned by the caller.  Return value 0 means success;
+ * a non-zero value is an SF_ERR_* code (argument errors) or a hipError_t
+ * offset by SF_ERR_HIP_BASE.  sf_error_string() names either kind.
+ *
+ * Data types: "bf16" buffers hold IEEE bfloat16 bit patterns (uint16_t);
+ * integer buffers are little-endian.  Streams are hipStream_t passed as an
+ * opaque pointer (NULL = the legacy default stream).
+ *
+ * Reference interfaces replaced (paths relative to the SpecFit tree; "tf:" is
+ * transformers/models/qwen3_moe/modeling_qwen3_moe.py of the pinned
+ * transformers release):
+ *   sf_router_topk       tf:258-267  Qwen3MoeTopKRouter.forward
+ *   sf_dispatch          src/specfit/runtime/qwen3_offloaded_experts.py:173-178
+ *                        (stable sort + unique_consecutive + route_tokens) and
+ *                        :111-113,120-122 (unique / where of the legacy path)
+ *   sf_grouped_swiglu    qwen3_offloaded_experts.py:38-62 (_expert_forward),
+ *                        :132-138 and :198 (routing-weight scale), :186-190
+ *                        (route gather)
+ *   sf_expert_swiglu     qwen3_offloaded_experts.py:38-62 (_expert_forward
+ *                        on already-gathered rows, no weight scale)
+ *   sf_combine           qwen3_offloaded_experts.py:144-164 and :200-202
+ *                        (index_add_ in canonical or arrival order)
+ *   sf_copy_h2d          src/specfit/runtime/gpu_expert_cache.py:556-561
+ *                        (slot.tensor.copy_(pinned_source, non_blocking=True))
+ */
+#ifndef SPECFIT_AMD_H
+#define SPECFIT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SF_ABI_VERSION 1
+
+/* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
+#define SF_OK 0
+#define SF_ERR_INVALID_ARGUMENT 1
+#define SF_ERR_UNSUPPORTED_SHAPE 2
+#define SF_ERR_MISALIGNED 3
+#define SF_ERR_TOO_MANY_EXPERTS 4
+#define SF_ERR_HIP_BASE 1000
+
+/* Largest expert count the router, dispatch and combine kernels accept. */
+#define SF_MAX_EXPERTS 256
+/* Largest top-k. */
+#define SF_MAX_TOPK 32
+
+typedef void *sf_stream_t;
+
+/* ABI version of the loaded library (SF_ABI_VERSION at build time). */
+int sf_abi_version(void);
+
+/* Static description of an error code; never NULL. */
+const char *sf_error_string(int code);
+
+/*
+ * K1: router.  Replaces Qwen3MoeTopKRouter.forward (tf:258-267).
+ *   logits[t,e] = bf16( sum_k hidden[t,k] * router_weight[e,k] )   (fp32 sum)
+ *   p[t,:]      = softmax_fp32(logits[t,:])
+ *   (v, idx)    = top_k(p[t,:]) in descending p; equal p -> lower expert id
+ *   w[t,j]      = bf16( v_j / (v_0 + ... + v_{k-1}) )   if norm_topk_prob
+ *               = bf16( v_j )                          otherwise
+ * The fp32 summation order of the dot product and of the softmax sum is
+ * fixed (see the kernel source), so logits, weights and indices are a pure
+ * function of the inputs.
+ *   hidden        bf16 [tokens, hidden_size]
+ *   router_weight bf16 [num_experts, hidden_size]
+ *   logits        bf16 [tokens, num_experts]          (output)
+ *   topk_weights  bf16 [tokens, top_k]                (output)
+ *   topk_index    int64 [tokens, top_k]               (output)
+ * Limits: 1 <= num_experts <= SF_MAX_EXPERTS, 1 <= top_k <= min(num_experts,
+ * SF_MAX_TOPK), hidden_size >= 1.  tokens == 0 launches nothing.
+ */
+int sf_router_topk(const void *hidden, const void *router_weight, int tokens,
+                   int hidden_size, int num_experts, int top_k,
+                   int norm_topk_prob, void *logits, void *topk_weights,
+                   int64_t *topk_index, sf_stream_t stream);
+
+/*
+ * K2: token-to-expert dispatch.  Replaces the stable sort of the flattened
+ * routes by expert id (qwen3_offloaded_experts.py:173-178).
+ *   topk_index int64 [tokens, top_k]
+ *   counts     int32 [num_experts + 1]  routes per expert; counts[num_experts]
+ *              = number of entries outside [0, num_experts) (not dispatched)
+ *   offsets    int32 [num_experts + 1]  exclusive prefix sum of counts
+ *   perm_pos   int32 [tokens * top_k]   route position (t * top_k + j) of each
+ *              permuted row; rows of one expert are contiguous and keep
+ *              ascending position order (stable)
+ *   inv_perm   int32 [tokens * top_k]   permuted row of each route position
+ *              (-1 for an out-of-range entry)
+ * One workgroup; any tokens >= 0.
+ */
+int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
+                int num_experts, int32_t *counts, int32_t *offsets,
+                int32_t *perm_pos, int32_t *inv_perm, sf_stream_t stream);
+
+/*
+ * K3: grouped SwiGLU expert MLP over dispatched rows.  Replaces the per-expert
+ * loop of _expert_forward + weight scale (qwen3_offloaded_experts.py:38-62,
+ * 132-138, 186-198).  For each listed expert e with rows
+ * r in [offsets[e], offsets[e+1]) and token t = perm_pos[r] / top_k:
+ *   gu   = bf16(hidden[t] . GU^T)          GU = packed[0 : 2*I*H] as [2I, H]
+ *   act  = bf16(bf16(silu(gu[:I])) * gu[I:])
+ *   y    = bf16(act . D^T)                 D  = packed[2*I*H :] as [H, I]
+ *   rows[r] = bf16(y * route_weights[perm_pos[r]])   (y if route_weights NULL)
+ * Packed expert layout: [gate (I x H) | up (I x H) | down (H x I)], row-major
+ * bf16, as written by the reference's packed checkpoint.
+ *   expert_ids      host int32 [n_experts]: experts computed by this call
+ *   expert_weights  host uint64 [n_experts]: device address of each expert's
+ *                   packed weights (a cache slot)
+ *   act_workspace   bf16 [tokens * top_k, intermediate_size] scratch
+ *   out_rows        bf16 [tokens * top_k, hidden_size] (rows of listed
+ *                   experts are written, others untouched)
+ * Experts of one call are independent; the result of an expert does not
+ * depend on which other experts share the call.
+ */
+int sf_grouped_swiglu(const void *hidden, const int32_t *perm_pos,
+                      const int32_t *offsets, const void *route_weights,
+                      int tokens, int top_k, int hidden_size,
+                      int intermediate_size, int n_experts,
+                      const int32_t *expert_ids,
+                      const uint64_t *expert_weights, void *act_workspace,
+                      void *out_rows, sf_stream_t stream);
+
+/*
+ * K3, device slot-table form: computes every expert e < num_experts whose
+ * slot_of_expert[e] >= 0 and that has at least one row, reading its weights
+ * at slot_base + slot_of_expert[e] * slot_stride_elems (bf16 elements).
+ * slot_of_expert is a device int32 [num_experts] array.  Needs no host-side
+ * knowledge of which experts are active (no device-to-host read).
+ */
+int sf_grouped_swiglu_table(const void *hidden, const int32_t *perm_pos,
+                            const int32_t *offsets, const void *route_weights,
+                            int tokens, int top_k, int hidden_size,
+                            int intermediate_size, int num_experts,
+                            const int32_t *slot_of_expert,
+                            const void *slot_base, int64_t slot_stride_elems,
+                            void *act_workspace, void *out_rows,
+                            sf_stream_t stream);
+
+/*
+ * K3 on already-gathered rows of one expert (the _expert_forward seam,
+ * qwen3_offloaded_experts.py:38-62): out[m, H] = y without weight scale.
+ *   rows bf16 [m, hidden_size] (row stride row_stride elements)
+ */
+int sf_expert_swiglu(const void *rows, int m, int64_t row_stride,
+                     int hidden_size, int intermediate_size,
+                     const void *packed_weights, void *act_workspace,
+                     void *out, sf_stream_t stream);
+
+/*
+ * K4: weighted combine.  Replaces zeros_like + index_add_ of the expert
+ * contributions (qwen3_offloaded_experts.py:144-164, 200-202).
+ *   out[t] = sum over the routes j of token t, in ascending
+ *            (expert_rank[topk_index[t,j]], j) order, of rows[inv_perm[t*K+j]]
+ * With accumulate_fp32 == 0 every addition rounds to bf16, exactly as
+ * sequential bf16 index_add_ calls; otherwise the sum is fp32 and rounded once.
+ *   rows         bf16 [tokens * top_k, hidden_size] (K3 output)
+ *   expert_rank  host int32 [num_experts] execution rank of each expert, or
+ *                NULL for canonical ascending expert id
+ *   out          bf16 [tokens, hidden_size]
+ */
+int sf_combine(const void *rows, const int64_t *topk_index,
+               const int32_t *inv_perm, const int32_t *expert_rank,
+               int tokens, int top_k, int num_experts, int hidden_size,
+               int accumulate_fp32, void *out, sf_stream_t stream);
+
+/*
+ * Host-to-device copy of an expert from pinned (page-locked) host memory into
+ * a cache slot, enqueued on `stream` (SDMA).  Replaces the non-blocking
+ * slot.tensor.copy_(pinned) of gpu_expert_cache.py:556-561.
+ */
+int sf_copy_h2d(void *device_dst, const void *host_src, size_t bytes,
+                sf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPECFIT_AMD_H */

@@ -1,0 +1,125 @@
+// K4: deterministic weighted combine (gather + add) in a fixed expert order.
+// Restates zeros_like + index_add_ of the per-expert contributions of the
+// reference (src/specfit/runtime/qwen3_offloaded_experts.py:144-164,
+// 200-202).  K3 already scaled every row by its routing weight, so the
+// combine only sums, per token, the rows of its routes.  The routes of a token
+// are visited in ascending (expert_rank[expert], position) order: canonical
+// mode ranks experts by id, arrival-order mode by execution order.  With bf16
+// accumulation each addition is rounded to bf16, which is what a sequence of
+// bf16 index_add_ calls computes; no atomics, so the result is bitwise
+// reproducible.
+#include "sf_common.h"
+
+namespace {
+
+constexpr int kCombineThreads = 256;
+constexpr int kColsPerThread = 8;
+constexpr int kColsPerBlock = kCombineThreads * kColsPerThread;
+
+struct RankTable {
+  int32_t rank[SF_MAX_EXPERTS];
+};
+
+template <bool kVec>
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(
+    const uint16_t* __restrict__ rows, const int64_t* __restrict__ idx,
+    const int32_t* __restrict__ inv_perm, const RankTable ranks, int use_rank,
+    int K, int E, int H, int acc_fp32, uint16_t* __restrict__ out) {
+  __shared__ int s_row[SF_MAX_TOPK];
+  const int t = blockIdx.x;
+  if (threadIdx.x == 0) {
+    // Order this token's routes: insertion sort on (rank, position).
+    int key[SF_MAX_TOPK];
+    int row[SF_MAX_TOPK];
+    int n = 0;
+    for (int j = 0; j < K; ++j) {
+      const int64_t e = idx[static_cast<int64_t>(t) * K + j];
+      const int r = inv_perm[static_cast<int64_t>(t) * K + j];
+      if (e < 0 || e >= E || r < 0) continue;
+      const int k = use_rank ? ranks.rank[e] : static_cast<int>(e);
+      int p = n++;
+      while (p > 0 && key[p - 1] > k) {  // equal keys keep position order
+        key[p] = key[p - 1];
+        row[p] = row[p - 1];
+        --p;
+      }
+      key[p] = k;
+      row[p] = r;
+    }
+    for (int j = 0; j < K; ++j) s_row[j] = j < n ? row[j] : -1;
+  }
+  __syncthreads();
+  const int c0 = blockIdx.y * kColsPerBlock + threadIdx.x * kColsPerThread;
+  if (c0 >= H) return;
+  float acc[kColsPerThread];
+#pragma unroll
+  for (int c = 0; c < kColsPerThread; ++c) acc[c] = 0.0f;
+  for (int j = 0; j < K; ++j) {
+    const int r = s_row[j];
+    if (r < 0) break;
+    const uint16_t* src = rows + static_cast<int64_t>(r) * H + c0;
+    uint16_t v[kColsPerThread];
+    if (kVec) {
+      const uint4 q = *reinterpret_cast<const uint4*>(src);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v[2 * c] = static_cast<uint16_t>(w[c] & 0xffffu);
+        v[2 * c + 1] = static_cast<uint16_t>(w[c] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < kColsPerThread; ++c) v[c] = c0 + c < H ? src[c] : 0;
+    }
+#pragma unroll
+    for (int c = 0; c < kColsPerThread; ++c) {
+      const float s = acc[c] + sf_bf16_to_f32(v[c]);
+      acc[c] = acc_fp32 ? s : sf_round_bf16(s);
+    }
+  }
+  uint16_t* dst = out + static_cast<int64_t>(t) * H + c0;
+  if (kVec) {
+    uint32_t w[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      w[c] = static_cast<uint32_t>(sf_f32_to_bf16(acc[2 * c])) |
+             (static_cast<uint32_t>(sf_f32_to_bf16(acc[2 * c + 1])) << 16);
+    *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < kColsPerThread; ++c)
+      if (c0 + c < H) dst[c] = sf_f32_to_bf16(acc[c]);
+  }
+}
+
+}  // namespace
+
+extern "C" int sf_combine(const void* rows, const int64_t* topk_index,
+                          const int32_t* inv_perm, const int32_t* expert_rank,
+                          int tokens, int top_k, int num_experts, int hidden_size,
+                          int accumulate_fp32, void* out, sf_stream_t stream) {
+  if (tokens < 0 || top_k < 1 || top_k > SF_MAX_TOPK || num_experts < 1 ||
+      num_experts > SF_MAX_EXPERTS || hidden_size < 1)
+    return SF_ERR_INVALID_ARGUMENT;
+  if (tokens == 0) return SF_OK;
+  if (!rows || !topk_index || !inv_perm || !out) return SF_ERR_INVALID_ARGUMENT;
+  RankTable ranks{};
+  if (expert_rank)
+    for (int e = 0; e < num_experts; ++e) ranks.rank[e] = expert_rank[e];
+  const bool vec = hidden_size % 8 == 0 && (reinterpret_cast<uintptr_t>(rows) & 15u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+  dim3 grid(tokens, (hidden_size + kColsPerBlock - 1) / kColsPerBlock);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (vec)
+    combine_kernel<true><<<grid, kCombineThreads, 0, s>>>(
+        static_cast<const uint16_t*>(rows), topk_index, inv_perm, ranks,
+        expert_rank != nullptr, top_k, num_experts, hidden_size, accumulate_fp32,
+        static_cast<uint16_t*>(out));
+  else
+    combine_kernel<false><<<grid, kCombineThreads, 0, s>>>(
+        static_cast<const uint16_t*>(rows), topk_index, inv_perm, ranks,
+        expert_rank != nullptr, top_k, num_experts, hidden_size, accumulate_fp32,
+        static_cast<uint16_t*>(out));
+  SF_LAUNCH_CHECK();
+  return SF_OK;
+}

@@ -1,0 +1,136 @@
+// K2: token-to-expert dispatch as a stable counting sort in LDS.
+// Restates the stable sort of the flattened routes by expert id plus
+// unique_consecutive / route_tokens of the reference
+// (src/specfit/runtime/qwen3_offloaded_experts.py:173-178).
+//
+// One workgroup of 1024 threads walks the N = tokens*top_k route positions in
+// chunks of 1024.  Per chunk every wavefront ranks its lanes among equal
+// expert ids with a ballot loop (rank = lanes below with the same id), the
+// per-wavefront counts are prefix-summed per expert in wavefront order, and
+// each route lands at offsets[e] + (routes of e in earlier chunks) +
+// (routes of e in earlier wavefronts) + rank.  This is exactly the ascending
+// position order inside every expert, i.e. a stable sort.
+#include "sf_common.h"
+
+namespace {
+
+constexpr int kDispatchThreads = 1024;
+constexpr int kDispatchWaves = kDispatchThreads / SF_WAVE;
+
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
+    const int64_t* __restrict__ idx, int N, int E, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm_pos,
+    int32_t* __restrict__ inv_perm) {
+  __shared__ int s_total[SF_MAX_EXPERTS];
+  __shared__ int s_offset[SF_MAX_EXPERTS + 1];
+  __shared__ int s_running[SF_MAX_EXPERTS];
+  __shared__ int s_wave_count[kDispatchWaves][SF_MAX_EXPERTS];
+  __shared__ int s_invalid;
+  const int tid = threadIdx.x;
+  const int lane = tid & (SF_WAVE - 1);
+  const int wave = tid / SF_WAVE;
+
+  for (int e = tid; e < SF_MAX_EXPERTS; e += kDispatchThreads) {
+    s_total[e] = 0;
+    s_running[e] = 0;
+  }
+  for (int i = tid; i < kDispatchWaves * SF_MAX_EXPERTS; i += kDispatchThreads)
+    (&s_wave_count[0][0])[i] = 0;
+  if (tid == 0) s_invalid = 0;
+  __syncthreads();
+
+  // Pass 1: histogram (integer atomics are order independent).
+  for (int i = tid; i < N; i += kDispatchThreads) {
+    int64_t e = idx[i];
+    if (e >= 0 && e < E)
+      atomicAdd(&s_total[e], 1);
+    else
+      atomicAdd(&s_invalid, 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+      s_offset[e] = run;
+      run += s_total[e];
+    }
+    s_offset[E] = run;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kDispatchThreads) {
+    counts[e] = s_total[e];
+    offsets[e] = s_offset[e];
+  }
+  if (tid == 0) {
+    counts[E] = s_invalid;
+    offsets[E] = s_offset[E];
+  }
+
+  // Pass 2: stable scatter, chunk by chunk.
+  const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (SF_WAVE - lane));
+  for (int base = 0; base < N; base += kDispatchThreads) {
+    const int i = base + tid;
+    int e = -1;
+    if (i < N) {
+      int64_t v = idx[i];
+      e = (v >= 0 && v < E) ? static_cast<int>(v) : -1;
+    }
+    const bool valid = e >= 0;
+    int rank = 0;
+    uint64_t pending = __ballot(valid);
+    while (pending) {
+      const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+      const int le = __shfl(e, leader, SF_WAVE);
+      const uint64_t same = __ballot(valid && e == le);
+      if (valid && e == le) rank = __popcll(same & lanes_below);
+      if (lane == leader) s_wave_count[wave][le] = __popcll(same);
+      pending &= ~same;
+    }
+    __syncthreads();
+    // Exclusive prefix over wavefronts, per expert, continuing the running
+    // count of earlier chunks.
+    for (int ex = tid; ex < E; ex += kDispatchThreads) {
+      int run = s_running[ex];
+      for (int w = 0; w < kDispatchWaves; ++w) {
+        int c = s_wave_count[w][ex];
+        s_wave_count[w][ex] = run;
+        run += c;
+      }
+      s_running[ex] = run;
+    }
+    __syncthreads();
+    if (i < N) {
+      if (valid) {
+        const int pos = s_offset[e] + s_wave_count[wave][e] + rank;
+        perm_pos[pos] = i;
+        inv_perm[i] = pos;
+      } else {
+        inv_perm[i] = -1;
+      }
+    }
+    __syncthreads();
+    // Reset the per-wavefront table for the next chunk.
+    for (int j = tid; j < kDispatchWaves * SF_MAX_EXPERTS; j += kDispatchThreads)
+      (&s_wave_count[0][0])[j] = 0;
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+extern "C" int sf_dispatch(const int64_t* topk_index, int tokens, int top_k,
+                           int num_experts, int32_t* counts, int32_t* offsets,
+                           int32_t* perm_pos, int32_t* inv_perm,
+                           sf_stream_t stream) {
+  if (tokens < 0 || top_k < 1 || num_experts < 1 || num_experts > SF_MAX_EXPERTS)
+    return SF_ERR_INVALID_ARGUMENT;
+  const long long n = static_cast<long long>(tokens) * top_k;
+  if (n > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
+  if (!counts || !offsets) return SF_ERR_INVALID_ARGUMENT;
+  if (n > 0 && (!topk_index || !perm_pos || !inv_perm)) return SF_ERR_INVALID_ARGUMENT;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dispatch_kernel<<<1, kDispatchThreads, 0, s>>>(topk_index, static_cast<int>(n), num_experts,
+                                                 counts, offsets, perm_pos, inv_perm);
+  SF_LAUNCH_CHECK();
+  return SF_OK;
+}

@@ -1,0 +1,312 @@
+"""PyTorch-facing wrappers of the C-ABI kernels (K1-K4 and the H2D copy).
+
+Tensors are plumbing: each wrapper checks dtype, device, shape and
+contiguity on the host, allocates outputs with the caching allocator and
+enqueues the HIP kernel on the caller's (default: current) stream through the
+C-ABI.  There is no PyTorch or CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Sequence
+
+import torch
+
+from . import _native
+
+_BF16 = torch.bfloat16
+
+
+class LaunchRecorder:
+    """Collects HIP timing events around K3 launches and H2D copies, each on
+    the stream the work runs on (enabled by ``record_launches``)."""
+
+    def __init__(self) -> None:
+        self.k3: list[tuple[int, int, str, torch.cuda.Event, torch.cuda.Event]] = []
+        self.h2d: list[tuple[int, torch.cuda.Event, torch.cuda.Event]] = []
+
+    @staticmethod
+    def _events(stream):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        return start, end
+
+
+_recorder: LaunchRecorder | None = None
+
+
+class record_launches:
+    """Context manager: ``with record_launches() as rec: ...``."""
+
+    def __enter__(self) -> LaunchRecorder:
+        global _recorder
+        if _recorder is not None:
+            raise RuntimeError("launch recording is already active")
+        _recorder = LaunchRecorder()
+        return _recorder
+
+    def __exit__(self, *exc) -> None:
+        global _recorder
+        _recorder = None
+
+
+def _stream_handle(stream: torch.cuda.Stream | None, device: torch.device) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream(device)
+    return int(s.cuda_stream)
+
+
+def _require_cuda(name: str, t: torch.Tensor, dtype: torch.dtype | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a HIP device")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must have dtype {dtype}")
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------------ K1 ----
+def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int,
+                norm_topk_prob: bool, *, stream: torch.cuda.Stream | None = None):
+    """(logits bf16 [T,E], weights bf16 [T,K], indices int64 [T,K]) of the
+    fused router kernel.  Replaces Qwen3MoeTopKRouter.forward (tf:258-267)."""
+    _require_cuda("hidden_states", hidden, _BF16)
+    _require_cuda("router weight", weight, _BF16)
+    if hidden.ndim != 2 or weight.ndim != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError("router expects hidden [T,H] and weight [E,H]")
+    if hidden.device != weight.device:
+        raise ValueError("router inputs must share a device")
+    hidden = hidden.contiguous()
+    weight = weight.contiguous()
+    T, H = hidden.shape
+    E = weight.shape[0]
+    logits = torch.empty((T, E), dtype=_BF16, device=hidden.device)
+    w = torch.empty((T, top_k), dtype=_BF16, device=hidden.device)
+    idx = torch.empty((T, top_k), dtype=torch.int64, device=hidden.device)
+    rc = _native.lib().sf_router_topk(
+        _ptr(hidden), _ptr(weight), T, H, E, int(top_k), int(bool(norm_topk_prob)),
+        _ptr(logits), _ptr(w), _ptr(idx), _stream_handle(stream, hidden.device))
+    _native.check(rc, "sf_router_topk")
+    return logits, w, idx
+
+
+# ------------------------------------------------------------------ K2 ----
+@dataclass
+class DispatchPlan:
+    """Device-side dispatch of one layer's routes (output of K2).
+
+    counts/offsets are int32 [E+1] (counts[E] = out-of-range entries),
+    perm_pos/inv_perm int32 [T*K].  ``host_counts`` is filled by
+    ``fetch_counts`` (the layer's one device-to-host read)."""
+
+    tokens: int
+    top_k: int
+    num_experts: int
+    counts: torch.Tensor
+    offsets: torch.Tensor
+    perm_pos: torch.Tensor
+    inv_perm: torch.Tensor
+    host_counts: torch.Tensor | None = None
+    ready: torch.cuda.Event | None = None
+
+    def fetch_counts(self) -> torch.Tensor:
+        """Copy counts+offsets to pinned host memory and wait for them."""
+        if self.host_counts is None:
+            pinned = torch.empty((2, self.num_experts + 1), dtype=torch.int32,
+                                 pin_memory=True)
+            pinned[0].copy_(self.counts, non_blocking=True)
+            pinned[1].copy_(self.offsets, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.counts.device))
+            ev.synchronize()
+            self.host_counts = pinned
+        return self.host_counts
+
+    def active_experts(self) -> tuple[int, ...]:
+        counts = self.fetch_counts()[0]
+        if int(counts[self.num_experts]):
+            raise KeyError("routing index outside the expert range")
+        return tuple(int(e) for e in torch.nonzero(counts[: self.num_experts]).flatten().tolist())
+
+    def host_offsets(self) -> list[int]:
+        return self.fetch_counts()[1].tolist()
+
+
+def dispatch(index: torch.Tensor, num_experts: int, *,
+             stream: torch.cuda.Stream | None = None) -> DispatchPlan:
+    """Stable counting sort of the [T,K] routes by expert id (K2)."""
+    _require_cuda("top_k_index", index, torch.int64)
+    if index.ndim != 2:
+        raise ValueError("top_k_index must have shape [tokens, top_k]")
+    index = index.contiguous()
+    T, K = index.shape
+    dev = index.device
+    counts = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * K, dtype=torch.int32, device=dev)
+    inv = torch.empty(T * K, dtype=torch.int32, device=dev)
+    if T * K == 0:
+        counts.zero_()
+        offsets.zero_()
+        return DispatchPlan(T, K, int(num_experts), counts, offsets, perm, inv)
+    rc = _native.lib().sf_dispatch(_ptr(index), T, K, int(num_experts), _ptr(counts),
+                                   _ptr(offsets), _ptr(perm), _ptr(inv),
+                                   _stream_handle(stream, dev))
+    _native.check(rc, "sf_dispatch")
+    return DispatchPlan(T, K, int(num_experts), counts, offsets, perm, inv)
+
+
+# ------------------------------------------------------------------ K3 ----
+def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torch.Tensor | None,
+                   expert_ids: Sequence[int], expert_weights: Sequence[torch.Tensor],
+                   hidden_size: int, intermediate_size: int, act: torch.Tensor,
+                   out_rows: torch.Tensor, *, stream: torch.cuda.Stream | None = None,
+                   tag: str = "") -> None:
+    """Grouped SwiGLU over the dispatched rows of the listed experts (K3).
+    ``expert_weights[i]`` is the packed [3*H*I] bf16 weight tensor of
+    ``expert_ids[i]`` (a cache slot)."""
+    n = len(expert_ids)
+    if n != len(expert_weights):
+        raise ValueError("expert_ids and expert_weights differ in length")
+    if n == 0 or plan.tokens == 0:
+        return
+    numel = 3 * hidden_size * intermediate_size
+    N = plan.tokens * plan.top_k
+    if act.shape != (N, intermediate_size) or out_rows.shape != (N, hidden_size):
+        raise ValueError("workspace shapes do not match the dispatch plan")
+    if hidden.shape != (plan.tokens, hidden_size) or not hidden.is_contiguous():
+        raise ValueError("hidden_states must be contiguous [tokens, hidden]")
+    if route_weights is not None and (route_weights.dtype != _BF16 or route_weights.numel() != N
+                                      or not route_weights.is_contiguous()):
+        raise ValueError("route weights must be contiguous bf16 [tokens*top_k]")
+    id_arr = (ctypes.c_int32 * n)()
+    w_arr = (ctypes.c_uint64 * n)()
+    for i, (e, w) in enumerate(zip(expert_ids, expert_weights)):
+        if not 0 <= int(e) < plan.num_experts:
+            raise KeyError(f"unknown expert {e}")
+        if w.dtype != _BF16 or w.numel() != numel or not w.is_contiguous() or w.device != hidden.device:
+            raise ValueError(f"packed expert {e} must be contiguous bf16 with {numel} elements")
+        id_arr[i] = int(e)
+        w_arr[i] = w.data_ptr()
+    rec = _recorder
+    if rec is not None:
+        s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
+        start, end = rec._events(s)
+    rc = _native.lib().sf_grouped_swiglu(
+        _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
+        plan.tokens, plan.top_k, hidden_size, intermediate_size, n,
+        ctypes.cast(id_arr, ctypes.c_void_p), ctypes.cast(w_arr, ctypes.c_void_p),
+        _ptr(act), _ptr(out_rows), _stream_handle(stream, hidden.device))
+    _native.check(rc, "sf_grouped_swiglu")
+    if rec is not None:
+        end.record(s)
+        rows = 0
+        if plan.host_counts is not None:
+            counts = plan.host_counts[0]
+            rows = int(sum(int(counts[int(e)]) for e in expert_ids))
+        rec.k3.append((n, rows, tag, start, end))
+
+
+def grouped_swiglu_table(hidden: torch.Tensor, plan: DispatchPlan,
+                         route_weights: torch.Tensor | None, slot_of_expert: torch.Tensor,
+                         slot_storage: torch.Tensor, hidden_size: int, intermediate_size: int,
+                         act: torch.Tensor, out_rows: torch.Tensor, *,
+                         stream: torch.cuda.Stream | None = None) -> None:
+    """K3 over every expert whose device slot-table entry is >= 0 (no host
+    knowledge of the active set needed)."""
+    if plan.tokens == 0:
+        return
+    _require_cuda("slot_of_expert", slot_of_expert, torch.int32)
+    if slot_of_expert.numel() != plan.num_experts or not slot_of_expert.is_contiguous():
+        raise ValueError("slot_of_expert must be contiguous int32 [num_experts]")
+    numel = 3 * hidden_size * intermediate_size
+    if slot_storage.ndim != 2 or slot_storage.shape[1] != numel or slot_storage.dtype != _BF16:
+        raise ValueError("slot storage must be bf16 [slots, 3*H*I]")
+    N = plan.tokens * plan.top_k
+    if act.shape != (N, intermediate_size) or out_rows.shape != (N, hidden_size):
+        raise ValueError("workspace shapes do not match the dispatch plan")
+    rc = _native.lib().sf_grouped_swiglu_table(
+        _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
+        plan.tokens, plan.top_k, hidden_size, intermediate_size, plan.num_experts,
+        _ptr(slot_of_expert), _ptr(slot_storage), int(slot_storage.stride(0)),
+        _ptr(act), _ptr(out_rows), _stream_handle(stream, hidden.device))
+    _native.check(rc, "sf_grouped_swiglu_table")
+
+
+def expert_swiglu(rows: torch.Tensor, packed: torch.Tensor, hidden_size: int,
+                  intermediate_size: int, *, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """y = SwiGLU expert MLP of already-gathered rows (no routing weight)."""
+    _require_cuda("hidden_states", rows, _BF16)
+    _require_cuda("packed expert", packed, _BF16)
+    if rows.ndim != 2 or rows.shape[1] != hidden_size:
+        raise ValueError("rows must have shape [m, hidden]")
+    expected = 3 * hidden_size * intermediate_size
+    if packed.numel() != expected:
+        raise ValueError(f"packed expert has {packed.numel()} elements, expected {expected}")
+    if rows.stride(1) != 1:
+        rows = rows.contiguous()
+    packed = packed.contiguous()
+    m = rows.shape[0]
+    out = torch.empty((m, hidden_size), dtype=_BF16, device=rows.device)
+    if m == 0:
+        return out
+    act = torch.empty((m, intermediate_size), dtype=_BF16, device=rows.device)
+    rc = _native.lib().sf_expert_swiglu(_ptr(rows), m, int(rows.stride(0)), hidden_size,
+                                        intermediate_size, _ptr(packed), _ptr(act), _ptr(out),
+                                        _stream_handle(stream, rows.device))
+    _native.check(rc, "sf_expert_swiglu")
+    return out
+
+
+# ------------------------------------------------------------------ K4 ----
+def combine(rows: torch.Tensor, index: torch.Tensor, plan: DispatchPlan, hidden_size: int,
+            *, expert_rank: Sequence[int] | None = None, accumulate_fp32: bool = False,
+            out: torch.Tensor | None = None,
+            stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """out[t] = sum of token t's scaled expert rows in canonical (or
+    ``expert_rank``) order (K4)."""
+    T, K = plan.tokens, plan.top_k
+    if out is None:
+        out = torch.empty((T, hidden_size), dtype=_BF16, device=index.device)
+    if T == 0:
+        return out
+    if rows.shape != (T * K, hidden_size) or rows.dtype != _BF16 or not rows.is_contiguous():
+        raise ValueError("rows must be contiguous bf16 [tokens*top_k, hidden]")
+    if out.shape != (T, hidden_size) or not out.is_contiguous() or out.dtype != _BF16:
+        raise ValueError("out must be contiguous bf16 [tokens, hidden]")
+    index = index.contiguous()
+    rank_arg = None
+    if expert_rank is not None:
+        if len(expert_rank) != plan.num_experts:
+            raise ValueError("expert_rank must hold one rank per expert")
+        rank_arg = ctypes.cast((ctypes.c_int32 * plan.num_experts)(*expert_rank), ctypes.c_void_p)
+    rc = _native.lib().sf_combine(_ptr(rows), _ptr(index), _ptr(plan.inv_perm), rank_arg, T, K,
+                                  plan.num_experts, hidden_size, int(bool(accumulate_fp32)),
+                                  _ptr(out), _stream_handle(stream, out.device))
+    _native.check(rc, "sf_combine")
+    return out
+
+
+# ------------------------------------------------------------- H2D copy ----
+def copy_h2d(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) -> None:
+    """Enqueue dst <- src (pinned host) on ``stream`` (hipMemcpyAsync/SDMA)."""
+    if src.device.type != "cpu" or dst.device.type != "cuda":
+        raise ValueError("copy_h2d copies host memory into a device tensor")
+    if not (src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("copy_h2d needs contiguous tensors")
+    nbytes = src.numel() * src.element_size()
+    if nbytes != dst.numel() * dst.element_size():
+        raise ValueError("copy_h2d size mismatch")
+    rec = _recorder
+    if rec is not None:
+        start, end = rec._events(stream)
+    rc = _native.lib().sf_copy_h2d(_ptr(dst), _ptr(src), nbytes, int(stream.cuda_stream))
+    _native.check(rc, "sf_copy_h2d")
+    if rec is not None:
+        end.record(stream)
+        rec.h2d.append((nbytes, start, end))

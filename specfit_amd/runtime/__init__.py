@@ -1,0 +1,22 @@
+"""Drop-in runtime of the offloaded Qwen3-MoE verification path
+(mirrors the public names of the reference's ``specfit.runtime``)."""
+from .cache_observer import (CacheTransition, CacheTransitionCounters, CacheTransitionObserver,
+                             RecordingCacheTransitionObserver,
+                             aggregate_cache_transition_counters)
+from .cache_snapshot import CacheSlotSnapshot, GpuExpertCacheSnapshot, PendingTransferSnapshot
+from .gpu_expert_cache import GpuExpertCache
+from .lease import ExpertCacheStats, ExpertLease, NoEvictableSlotError
+from .qwen3_offloaded_experts import (ExpertExecutionPolicy, Qwen3OffloadedExperts,
+                                      ReductionMode)
+from .qwen3_router import Qwen3MoeTopKRouterHip
+from .state import ExpertKey
+from .trace import RuntimeEventKind
+
+__all__ = [
+    "CacheSlotSnapshot", "CacheTransition", "CacheTransitionCounters",
+    "CacheTransitionObserver", "ExpertCacheStats", "ExpertExecutionPolicy", "ExpertKey",
+    "ExpertLease", "GpuExpertCache", "GpuExpertCacheSnapshot", "NoEvictableSlotError",
+    "PendingTransferSnapshot", "Qwen3MoeTopKRouterHip", "Qwen3OffloadedExperts",
+    "RecordingCacheTransitionObserver", "ReductionMode", "RuntimeEventKind",
+    "aggregate_cache_transition_counters",
+]

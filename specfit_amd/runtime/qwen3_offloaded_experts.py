@@ -1,0 +1,358 @@
+"""Offloaded Qwen3-MoE expert operator on the gfx950 kernels.
+
+Drop-in for src/specfit/runtime/qwen3_offloaded_experts.py:19-292
+(``ReductionMode``, ``ExpertExecutionPolicy``, ``Qwen3OffloadedExperts`` with
+the same constructor, ``forward`` signature and ValueErrors, and the
+``_expert_forward`` seam).
+
+One layer forward:
+
+1. K2 ``sf_dispatch`` stably sorts the T*K routes by expert id on the device
+   (replaces torch.sort / unique_consecutive / where, :111-122, :173-178); the
+   host reads the [E+1] counts once (the layer's only device-to-host sync --
+   the reference has the same one) to know the active experts.
+2. Experts are leased from the ``GpuExpertCache`` in the reference's order
+   and with its acquire / one-ahead prefetch / release sequence
+   (:205-230), so LRU state, generations, statistics and observer events
+   evolve exactly as in the reference.  Consecutive experts that need no
+   eviction (resident hits, in-flight joins) are computed by ONE grouped
+   SwiGLU launch (K3); their slots stay pinned until that launch is
+   enqueued, and the batch is always flushed before an acquisition that
+   chooses a victim, so every eviction decision sees the same leased set as
+   the reference.  A miss is computed by its own launch, ordered after its
+   H2D ready event on the GPU only (no host wait), so later copies stream
+   back to back on the copy stream while earlier experts compute.
+3. K3 writes bf16(y * routing weight) per dispatched row; K4 ``sf_combine``
+   adds each token's rows in canonical (ascending expert id) order with one
+   fp32 accumulator (default) or, like the reference's sequence of bf16
+   ``index_add_`` calls (:140-164), with bf16 rounding per addition --
+   always so in arrival order.
+
+Every expert's result is independent of how experts are grouped into
+launches and of the execution order, so canonical outputs are bitwise
+invariant to order, slot count and prefetch policy.
+"""
+from __future__ import annotations
+
+from contextlib import closing
+from dataclasses import dataclass
+from enum import Enum
+from typing import Sequence
+
+import torch
+from torch import nn
+
+from .. import ops
+from .gpu_expert_cache import GpuExpertCache
+from .lease import ExpertLease, NoEvictableSlotError
+from .state import ExpertKey
+
+
+# Largest number of experts one K3 launch of the legacy path computes.
+_MAX_BATCH = 32
+
+
+class ReductionMode(str, Enum):
+    CANONICAL = "canonical"
+    ARRIVAL_ORDER = "arrival_order"
+
+
+class ExpertExecutionPolicy(str, Enum):
+    EXPERT_ID_ASCENDING = "expert_id_ascending"
+    RESIDENT_FIRST = "resident_first"
+
+
+@dataclass
+class _GroupedRoutes:
+    """Device buffers of one layer forward shared by its K3 launches."""
+
+    hidden: torch.Tensor          # bf16 [T, H] contiguous
+    plan: ops.DispatchPlan
+    route_weights: torch.Tensor   # bf16 [T*K] contiguous
+    act: torch.Tensor             # bf16 [T*K, I] scratch
+    rows: torch.Tensor            # bf16 [T*K, H] scaled expert outputs
+    expert_ids: Sequence[int] = ()
+    tag: str = ""                 # "resident" or "miss": label of the launch
+
+
+def _dispatch(top_k_index: torch.Tensor, num_experts: int) -> ops.DispatchPlan:
+    """Seam: K2 dispatch of one layer's routes."""
+    return ops.dispatch(top_k_index, num_experts)
+
+
+def _expert_forward(hidden_states: torch.Tensor, packed_weights, *, hidden_size: int,
+                    intermediate_size: int, routes: _GroupedRoutes | None = None) -> torch.Tensor:
+    """Seam for every expert MLP launch (qwen3_offloaded_experts.py:38-62).
+
+    Without ``routes``: the reference signature -- ``hidden_states`` are the
+    gathered rows of one expert and ``packed_weights`` its packed
+    ``[gate | up | down]`` tensor; returns the unscaled SwiGLU output.
+    With ``routes``: ``packed_weights`` is a sequence of slot tensors for
+    ``routes.expert_ids``; K3 writes their weighted rows into ``routes.rows``.
+    """
+    projection = hidden_size * intermediate_size
+    if routes is None:
+        if packed_weights.numel() != 3 * projection:
+            raise ValueError(f"packed expert has {packed_weights.numel()} elements, "
+                             f"expected {3 * projection}")
+        return ops.expert_swiglu(hidden_states, packed_weights, hidden_size, intermediate_size)
+    ops.grouped_swiglu(routes.hidden, routes.plan, routes.route_weights, routes.expert_ids,
+                       packed_weights, hidden_size, intermediate_size, routes.act, routes.rows,
+                       tag=routes.tag)
+    return routes.rows
+
+
+class Qwen3OffloadedExperts(nn.Module):
+    """Routed experts of one decoder layer served from a GpuExpertCache."""
+
+    def __init__(self, *, layer_id: int, cache: GpuExpertCache, hidden_size: int,
+                 intermediate_size: int,
+                 reduction_mode: ReductionMode | str = ReductionMode.CANONICAL,
+                 execution_policy: ExpertExecutionPolicy | str = (
+                     ExpertExecutionPolicy.EXPERT_ID_ASCENDING),
+                 h2d_prefetch: bool = True, combine_fp32: bool = True) -> None:
+        super().__init__()
+        if layer_id < 0:
+            raise ValueError("layer_id must be non-negative")
+        if hidden_size <= 0:
+            raise ValueError("hidden_size must be positive")
+        if intermediate_size <= 0:
+            raise ValueError("intermediate_size must be positive")
+        if type(h2d_prefetch) is not bool:
+            raise ValueError("h2d_prefetch must be a boolean")
+        if type(combine_fp32) is not bool:
+            raise ValueError("combine_fp32 must be a boolean")
+        self.layer_id = layer_id
+        self.cache = cache
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+        self.reduction_mode = ReductionMode(reduction_mode)
+        self.execution_policy = ExpertExecutionPolicy(execution_policy)
+        self.h2d_prefetch = h2d_prefetch
+        # Canonical reduction accumulates in fp32 and rounds once (max error
+        # against the fp32 layer ~6e-3 instead of ~1e-2 for per-addition bf16
+        # rounding); arrival order always rounds every addition to bf16, the
+        # order-dependent arithmetic that mode exists to reproduce.
+        self.combine_fp32 = combine_fp32
+        self._prediction_scheduler = None
+        self._num_experts: int | None = None
+
+    # -------------------------------------------------------------- forward --
+    def forward(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
+                top_k_weights: torch.Tensor, *,
+                execution_order: Sequence[int] | None = None) -> torch.Tensor:
+        self._validate_inputs(hidden_states, top_k_index, top_k_weights)
+        if self._prediction_scheduler is not None:
+            if execution_order is not None:
+                raise ValueError("explicit execution_order conflicts with dynamic predicted prefetch")
+            return self._forward_prefetched(hidden_states, top_k_index, top_k_weights)
+        routes, active = self._prepare(hidden_states, top_k_index, top_k_weights)
+        order = self._resolve_execution_order(active, execution_order)
+        if routes is None:
+            return torch.zeros_like(hidden_states)
+        self._run_in_order(order, routes)
+        if self.reduction_mode is ReductionMode.ARRIVAL_ORDER:
+            return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
+                               expert_rank=self._arrival_ranks(order), accumulate_fp32=False)
+        return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
+                           accumulate_fp32=self.combine_fp32)
+
+    def _forward_prefetched(self, hidden_states, top_k_index, top_k_weights):
+        """Scheduler-driven forward (qwen3_offloaded_experts.py:166-203): the
+        scheduler yields leased experts in the order it chooses (ready
+        transfers first) and releases each lease when resumed, so every
+        yielded expert is launched before control returns to it.  Outputs
+        are reduced canonically."""
+        routes, active = self._prepare(hidden_states, top_k_index, top_k_weights)
+        scheduled = self._prediction_scheduler.experts(self.layer_id, active)
+        stream = torch.cuda.current_stream(self.cache.device)
+        with closing(scheduled):
+            for expert_id, lease in scheduled:
+                if routes is None:
+                    raise RuntimeError("scheduler yielded an expert for an empty layer")
+                weights = lease.wait(stream)
+                routes.expert_ids = [expert_id]
+                routes.tag = "scheduled"
+                _expert_forward(routes.hidden, [weights], hidden_size=self.hidden_size,
+                                intermediate_size=self.intermediate_size, routes=routes)
+        if routes is None:
+            return torch.zeros_like(hidden_states)
+        return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
+                           accumulate_fp32=self.combine_fp32)
+
+    # ------------------------------------------------------------- helpers --
+    def num_experts(self) -> int:
+        """Expert count of this layer: 1 + the largest expert id among the
+        cache's sources for this layer."""
+        if self._num_experts is None:
+            ids = [k.expert_id for k in self.cache._sources
+                   if isinstance(k, ExpertKey) and k.layer_id == self.layer_id]
+            if not ids:
+                raise ValueError(f"cache holds no experts of layer {self.layer_id}")
+            n = max(ids) + 1
+            if n > 256:
+                raise ValueError("at most 256 experts per layer are supported")
+            self._num_experts = n
+        return self._num_experts
+
+    def _prepare(self, hidden_states, top_k_index, top_k_weights):
+        """Dispatch on the device, read the active experts, allocate the
+        layer's row buffers.  Returns (routes or None when there are no
+        routes, active experts ascending)."""
+        T, K = top_k_index.shape
+        if hidden_states.dtype != torch.bfloat16:
+            raise ValueError("hidden_states must be bfloat16")
+        if T == 0 or K == 0:
+            return None, ()
+        num_experts = self.num_experts()
+        plan = _dispatch(top_k_index, num_experts)
+        counts = plan.fetch_counts()[0]
+        if int(counts[num_experts]):
+            self._raise_invalid_index(top_k_index, num_experts)
+        active = tuple(int(e) for e in torch.nonzero(counts[:num_experts]).flatten().tolist())
+        dev = hidden_states.device
+        routes = _GroupedRoutes(
+            hidden=hidden_states.contiguous(),
+            plan=plan,
+            route_weights=top_k_weights.to(torch.bfloat16).contiguous().reshape(-1),
+            act=torch.empty((T * K, self.intermediate_size), dtype=torch.bfloat16, device=dev),
+            rows=torch.empty((T * K, self.hidden_size), dtype=torch.bfloat16, device=dev))
+        return routes, active
+
+    def _raise_invalid_index(self, top_k_index, num_experts) -> None:
+        values = top_k_index.flatten().tolist()
+        bad = next(v for v in values if v < 0 or v >= num_experts)
+        ExpertKey(self.layer_id, int(bad))  # negative ids raise ValueError here
+        raise KeyError(f"unknown expert {ExpertKey(self.layer_id, int(bad))!r}")
+
+    def _arrival_ranks(self, order: Sequence[int]) -> list[int]:
+        """Execution position of each expert (combine order of ARRIVAL_ORDER)."""
+        rank = [0] * self.num_experts()
+        for position, expert in enumerate(order):
+            rank[expert] = position
+        return rank
+
+    def _launch(self, routes: _GroupedRoutes, batch: list[tuple[int, ExpertLease, torch.Tensor]],
+                tag: str = "") -> None:
+        """One K3 launch for a batch of waited leases, then unpin them."""
+        try:
+            routes.expert_ids = [e for e, _, _ in batch]
+            routes.tag = tag
+            _expert_forward(routes.hidden, [w for _, _, w in batch],
+                            hidden_size=self.hidden_size,
+                            intermediate_size=self.intermediate_size, routes=routes)
+        finally:
+            for _, lease, _ in batch:
+                lease._unpin()
+
+    def _run_in_order(self, order: tuple[int, ...], routes: _GroupedRoutes) -> None:
+        """Reference lease sequence (acquire, optional one-ahead prefetch,
+        wait, release) with the K3 launches batched.
+
+        A released expert's slot stays pinned until its batch is launched.
+        Pinned slots were all touched after every unpinned slot, so as long
+        as one unleased, unpinned slot exists the LRU victim of the next
+        miss is the same slot the reference would pick; otherwise the batch
+        is launched first.  Batches are also capped at ``_MAX_BATCH``."""
+        cache = self.cache
+        stream = torch.cuda.current_stream(cache.device)
+        batch: list[tuple[int, ExpertLease, torch.Tensor]] = []
+        # Misses are launched in groups of about a third of the slots so the
+        # copy stream never waits for the kernel of the group being filled.
+        miss_group = max(1, cache.slot_count // 3)
+        misses = 0
+
+        def flush() -> None:
+            nonlocal misses
+            if batch:
+                pending_batch = list(batch)
+                tag = "miss" if misses else "resident"
+                batch.clear()
+                misses = 0
+                self._launch(routes, pending_batch, tag)
+
+        def before_acquire(k: ExpertKey, *, split_resident_run: bool) -> bool:
+            """Flush if the eviction could differ (or, when asked, to keep a
+            run of resident experts in its own launch); True when k misses."""
+            if cache.is_available(k):
+                return False
+            if batch and ((split_resident_run and misses == 0) or not cache.has_unleased_slot()):
+                flush()
+            return True
+
+        ahead: ExpertLease | None = None
+        ahead_missed = False
+        try:
+            for index, expert_id in enumerate(order):
+                current, ahead = ahead, None
+                missed, ahead_missed = ahead_missed, False
+                if current is None:
+                    k = ExpertKey(self.layer_id, expert_id)
+                    missed = before_acquire(k, split_resident_run=True)
+                    current = cache.acquire(k)
+                try:
+                    if self.h2d_prefetch and index + 1 < len(order):
+                        nxt = ExpertKey(self.layer_id, order[index + 1])
+                        will_miss = before_acquire(nxt, split_resident_run=False)
+                        try:
+                            ahead = cache._prefetch(nxt)
+                            ahead_missed = will_miss
+                        except NoEvictableSlotError:
+                            pass
+                    weights = current.wait(stream)
+                except BaseException:
+                    current.release()
+                    raise
+                batch.append((expert_id, current, weights))
+                current._release_keep_pinned()
+                misses += int(missed)
+                if (len(batch) >= _MAX_BATCH or misses >= miss_group
+                        or (misses == 0 and ahead_missed)):
+                    flush()
+            flush()
+        except BaseException:
+            for _, lease, _ in batch:
+                lease._unpin()
+            batch.clear()
+            raise
+        finally:
+            if ahead is not None:
+                ahead.release()
+
+    def _validate_inputs(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
+                         top_k_weights: torch.Tensor) -> None:
+        if hidden_states.ndim != 2:
+            raise ValueError("hidden_states must have shape [tokens, hidden]")
+        if hidden_states.shape[1] != self.hidden_size:
+            raise ValueError(f"hidden_states width is {hidden_states.shape[1]}, "
+                             f"expected {self.hidden_size}")
+        if top_k_index.ndim != 2:
+            raise ValueError("top_k_index must have shape [tokens, top_k]")
+        if top_k_weights.shape != top_k_index.shape:
+            raise ValueError("top_k_weights must match top_k_index shape")
+        if top_k_index.shape[0] != hidden_states.shape[0]:
+            raise ValueError("routing tensors must match the token count")
+        if top_k_index.dtype is not torch.long:
+            raise ValueError("top_k_index must use torch.long")
+        if hidden_states.device != self.cache.device:
+            raise ValueError("hidden_states must be on the cache device")
+        if top_k_index.device != hidden_states.device:
+            raise ValueError("top_k_index must be on the hidden-state device")
+        if top_k_weights.device != hidden_states.device:
+            raise ValueError("top_k_weights must be on the hidden-state device")
+
+    def _resolve_execution_order(self, active_experts: tuple[int, ...],
+                                 execution_order: Sequence[int] | None) -> tuple[int, ...]:
+        if execution_order is not None:
+            order = tuple(int(e) for e in execution_order)
+            if len(order) != len(set(order)):
+                raise ValueError("execution_order must not contain duplicates")
+            if set(order) != set(active_experts):
+                raise ValueError("execution_order must contain every active expert exactly once")
+            return order
+        if self.execution_policy is ExpertExecutionPolicy.EXPERT_ID_ASCENDING:
+            return active_experts
+        resident = frozenset(self.cache.resident_expert_ids())
+        hits = tuple(e for e in active_experts if ExpertKey(self.layer_id, e) in resident)
+        misses = tuple(e for e in active_experts if ExpertKey(self.layer_id, e) not in resident)
+        return hits + misses
