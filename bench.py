@@ -42,6 +42,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU-baseline sample (0 disables it)")
     p.add_argument("--resident-reps", type=int, default=50)
+    p.add_argument("--record", choices=("full", "k3", "none"), default="full",
+                   help="timing events in the timed region: K3 launches + one copy window "
+                        "per step (full), K3 only, or none")
     return p.parse_args()
 
 
@@ -86,6 +89,20 @@ def cpu_baseline(layer, hidden_list, seconds: float) -> dict | None:
                        f"workload ({elapsed:.1f}s): oracle router (C, 1 thread) + numpy bf16-eager "
                        f"expert loop (BLAS {blas_threads} threads) + C combine"),
             "cpu_model": _cpu_model()}
+
+
+def _union_length(spans) -> float:
+    total, cur_s, cur_e = 0.0, None, None
+    for s_, e_ in sorted(spans):
+        if cur_e is None or s_ > cur_e:
+            if cur_e is not None:
+                total += cur_e - cur_s
+            cur_s, cur_e = s_, e_
+        else:
+            cur_e = max(cur_e, e_)
+    if cur_e is not None:
+        total += cur_e - cur_s
+    return total
 
 
 def _cpu_model() -> str:
@@ -154,13 +171,23 @@ def main() -> int:
 
     before = cache.stats()
     timed = hidden[args.prewarm + args.warmup:]
-    with ops.record_launches() as rec:
+    if args.record == "none":
+        rec = ops.LaunchRecorder(copies=False)
         torch.cuda.synchronize()
         start = time.perf_counter()
         for h in timed:
             step(h)
         torch.cuda.synchronize()
         wall = time.perf_counter() - start
+    else:
+        with ops.record_launches(copies=args.record == "full") as rec:
+            torch.cuda.synchronize()
+            start = time.perf_counter()
+            for h in timed:
+                step(h)
+                rec.close_copy_window()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - start
     after = cache.stats()
     misses = after.h2d_submissions - before.h2d_submissions
     hits = after.resident_hits - before.resident_hits
@@ -178,12 +205,20 @@ def main() -> int:
     res = [x for x in k3 if x[2] == "resident"]
     res_bytes = sum(k3_bytes(n, r) for n, r, _, _ in res)
     res_time = sum(x[3] for x in res)
-    h2d = [(b, s.elapsed_time(e) * 1e-3) for b, s, e in rec.h2d]
-    h2d_bytes = sum(b for b, _ in h2d)
-    h2d_time = sum(t for _, t in h2d)
+    h2d_bytes = misses * expert_bytes
+    h2d_time = rec.copy_busy_seconds() if rec.windows else 0.0
+    # Overlap of transfers and expert GEMMs: (t_h2d + t_gemm - t_union) /
+    # min(t_h2d, t_gemm), with t_union the measured union of the copy windows
+    # and the K3 launch intervals (all events share the device clock).
     overlap = None
-    if h2d_time > 0 and k3_time > 0:
-        overlap = max(0.0, min(1.0, (h2d_time + k3_time - wall) / min(h2d_time, k3_time)))
+    if rec.windows and rec.k3:
+        origin = rec.windows[0][0]
+        spans_copy = [(origin.elapsed_time(a), origin.elapsed_time(b)) for a, b in rec.windows]
+        spans_k3 = [(origin.elapsed_time(a), origin.elapsed_time(b)) for *_, a, b in rec.k3]
+        t_union = _union_length(spans_copy + spans_k3) * 1e-3
+        t_gemm = _union_length(spans_k3) * 1e-3
+        t_h2d = _union_length(spans_copy) * 1e-3
+        overlap = max(0.0, min(1.0, (t_h2d + t_gemm - t_union) / min(t_h2d, t_gemm)))
 
     # Host-link peak: best of 10 x 1 GiB pinned -> device copies.
     flat = layer.experts.view(-1)
@@ -255,6 +290,7 @@ def main() -> int:
                    "tokens": T, "hidden": H, "experts": E, "top_k": K, "intermediate": I,
                    "cache_slots": slots, "prewarm_cycles": args.prewarm,
                    "execution_policy": "resident_first", "h2d_prefetch": True},
+        "record": args.record,
         "roofline": {"bound": "hbm", "achieved": k3_achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": k3_achieved / HBM_PEAK_GBS, "traffic": None,
                      "kernel": "K3 grouped SwiGLU (gateup_mfma + down_mfma dispatches)",
@@ -262,10 +298,13 @@ def main() -> int:
                      "alg_bytes_per_launch": k3_alg / max(len(k3), 1)},
         "cpu_baseline": cpu,
         "h2d": {"achieved_gbs": h2d_bytes / h2d_time / 1e9 if h2d_time else None,
-                "link_peak_gbs": best, "transfers": len(h2d), "bytes": h2d_bytes,
-                "busy_ms": h2d_time * 1e3},
+                "link_peak_gbs": best, "transfers": misses, "bytes": h2d_bytes,
+                "busy_ms": h2d_time * 1e3,
+                "note": "busy = union over steps of [first copy start, last copy end] on the two "
+                        "copy streams"},
         "cache": {"misses_per_step": misses / args.steps, "hits_per_step": hits / args.steps},
         "overlap": overlap,
+        "h2d_link_busy_frac": h2d_time / wall if h2d_time else None,
         "k3_resident_in_step": {"launches": len(res), "gbs": res_bytes / res_time / 1e9 if res_time else None},
         "k3_all_resident": {"experts": len(active), "rows": rows_n, "us": res_launch * 1e6,
                             "gbs": res_launch_bytes / res_launch / 1e9,

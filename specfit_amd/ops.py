@@ -22,9 +22,53 @@ class LaunchRecorder:
     """Collects HIP timing events around K3 launches and H2D copies, each on
     the stream the work runs on (enabled by ``record_launches``)."""
 
-    def __init__(self) -> None:
+    def __init__(self, *, copies: bool = True) -> None:
         self.k3: list[tuple[int, int, str, torch.cuda.Event, torch.cuda.Event]] = []
-        self.h2d: list[tuple[int, torch.cuda.Event, torch.cuda.Event]] = []
+        # Copies are timed per window (first copy start .. last copy end of a
+        # window, per stream), not per copy: ``close_copy_window`` ends one.
+        self.copies = copies
+        self.h2d_bytes = 0
+        self.h2d_count = 0
+        self.windows: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+        self._open: dict[int, tuple[torch.cuda.Stream, torch.cuda.Event]] = {}
+
+    def _copy_started(self, stream: torch.cuda.Stream, nbytes: int) -> None:
+        self.h2d_bytes += nbytes
+        self.h2d_count += 1
+        key = int(stream.cuda_stream)
+        if self.copies and key not in self._open:
+            start = torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            self._open[key] = (stream, start)
+
+    def close_copy_window(self) -> None:
+        for stream, start in self._open.values():
+            end = torch.cuda.Event(enable_timing=True)
+            end.record(stream)
+            self.windows.append((start, end))
+        self._open.clear()
+
+    def copy_busy_seconds(self) -> float:
+        """Sum over windows of the copy-stream busy interval (windows of the
+        two SDMA streams overlap in time; their union is returned)."""
+        spans = []
+        origin = None
+        for start, end in self.windows:
+            if origin is None:
+                origin = start
+            spans.append((origin.elapsed_time(start), origin.elapsed_time(end)))
+        spans.sort()
+        total, cur_s, cur_e = 0.0, None, None
+        for s_, e_ in spans:
+            if cur_e is None or s_ > cur_e:
+                if cur_e is not None:
+                    total += cur_e - cur_s
+                cur_s, cur_e = s_, e_
+            else:
+                cur_e = max(cur_e, e_)
+        if cur_e is not None:
+            total += cur_e - cur_s
+        return total * 1e-3
 
     @staticmethod
     def _events(stream):
@@ -40,11 +84,14 @@ _recorder: LaunchRecorder | None = None
 class record_launches:
     """Context manager: ``with record_launches() as rec: ...``."""
 
+    def __init__(self, *, copies: bool = True) -> None:
+        self._copies = copies
+
     def __enter__(self) -> LaunchRecorder:
         global _recorder
         if _recorder is not None:
             raise RuntimeError("launch recording is already active")
-        _recorder = LaunchRecorder()
+        _recorder = LaunchRecorder(copies=self._copies)
         return _recorder
 
     def __exit__(self, *exc) -> None:
@@ -302,11 +349,7 @@ def copy_h2d(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) ->
     nbytes = src.numel() * src.element_size()
     if nbytes != dst.numel() * dst.element_size():
         raise ValueError("copy_h2d size mismatch")
-    rec = _recorder
-    if rec is not None:
-        start, end = rec._events(stream)
+    if _recorder is not None:
+        _recorder._copy_started(stream, nbytes)
     rc = _native.lib().sf_copy_h2d(_ptr(dst), _ptr(src), nbytes, int(stream.cuda_stream))
     _native.check(rc, "sf_copy_h2d")
-    if rec is not None:
-        end.record(stream)
-        rec.h2d.append((nbytes, start, end))

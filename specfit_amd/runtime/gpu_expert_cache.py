@@ -133,10 +133,18 @@ class GpuExpertCache:
 
         with torch.cuda.device(self.device):
             self.copy_stream = torch.cuda.Stream(device=self.device)
+            # A second SDMA stream: consecutive transfers alternate between the
+            # two so one engine's per-transfer setup overlaps the other's data
+            # movement (9 MiB copies reach ~98% of the host-link peak instead
+            # of ~92% on one stream).  Used only while copy_stream is the
+            # cache's own stream.
+            self._own_copy_stream = self.copy_stream
+            self._aux_copy_stream = torch.cuda.Stream(device=self.device)
             storage = torch.empty((slot_count, *shape), dtype=dtype, device=self.device)
             # The allocation may be recycled memory whose earlier readers are
             # still queued on the current stream: order the first copy after them.
             self.copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+            self._aux_copy_stream.wait_stream(torch.cuda.current_stream(self.device))
         self.cache_id = cache_id or f"cuda-{self.device.index}-stream-{int(self.copy_stream.cuda_stream)}"
         self.queue_id = queue_id or f"{self.cache_id}-copy"
         self._storage = storage
@@ -460,7 +468,11 @@ class GpuExpertCache:
         slot.expert_id = expert_id
         guards = tuple(slot.use_events.values())
         slot.use_events.clear()
-        stream = self.copy_stream
+        stream = self._transfer_stream()
+        if slot.ready_event is not None:
+            # Writes of one slot stay in submission order even when the
+            # previous one ran on the other stream.
+            stream.wait_event(slot.ready_event)
         for guard in guards:
             stream.wait_event(guard)
         ops.copy_h2d(slot.tensor, self._sources[expert_id], stream)
@@ -480,6 +492,14 @@ class GpuExpertCache:
             self._record_transition(kind=RuntimeEventKind.H2D_SUBMIT, expert_id=expert_id,
                                     slot=slot, submission_sequence=transfer.submission_sequence,
                                     ready_event=ready)
+
+    def _transfer_stream(self) -> torch.cuda.Stream:
+        """Stream of the next H2D: alternate the cache's two SDMA streams by
+        submission sequence; a replaced copy_stream (a scheduler's shared
+        queue) takes every transfer."""
+        if self.copy_stream is not self._own_copy_stream or self._submission_sequence % 2 == 0:
+            return self.copy_stream
+        return self._aux_copy_stream
 
     def _reap_completed_transfers(self) -> None:
         """Publish completed transfers as resident, strictly in submission order."""
