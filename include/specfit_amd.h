@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 1
+#define SF_ABI_VERSION 2
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -115,6 +115,9 @@ int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
  *   rows[r] = bf16(y * route_weights[perm_pos[r]])   (y if route_weights NULL)
  * Packed expert layout: [gate (I x H) | up (I x H) | down (H x I)], row-major
  * bf16, as written by the reference's packed checkpoint.
+ *   max_rows        an upper bound on the rows of any listed expert (any
+ *                   value >= 1 is correct; tokens * top_k always is).  It
+ *                   picks the MFMA tile count per pass, i.e. only speed.
  *   expert_ids      host int32 [n_experts]: experts computed by this call
  *   expert_weights  host uint64 [n_experts]: device address of each expert's
  *                   packed weights (a cache slot)
@@ -127,7 +130,7 @@ int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
 int sf_grouped_swiglu(const void *hidden, const int32_t *perm_pos,
                       const int32_t *offsets, const void *route_weights,
                       int tokens, int top_k, int hidden_size,
-                      int intermediate_size, int n_experts,
+                      int intermediate_size, int n_experts, int max_rows,
                       const int32_t *expert_ids,
                       const uint64_t *expert_weights, void *act_workspace,
                       void *out_rows, sf_stream_t stream);

@@ -20,61 +20,88 @@ struct RankTable {
   int32_t rank[SF_MAX_EXPERTS];
 };
 
+__device__ __forceinline__ void unpack8(uint4 q, uint16_t* v) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    v[2 * c] = static_cast<uint16_t>(w[c] & 0xffffu);
+    v[2 * c + 1] = static_cast<uint16_t>(w[c] >> 16);
+  }
+}
+
+// One block per (token, 2048-column slice).  Threads 0..K-1 fetch the
+// token's routes in parallel; thread 0 orders them in LDS.  Up to
+// kPrefetch rows are then loaded before any addition so the gather costs one
+// memory round trip, and the additions run in the fixed order.
+constexpr int kPrefetch = 8;
+
 template <bool kVec>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
     const uint16_t* __restrict__ rows, const int64_t* __restrict__ idx,
     const int32_t* __restrict__ inv_perm, const RankTable ranks, int use_rank,
     int K, int E, int H, int acc_fp32, uint16_t* __restrict__ out) {
+  __shared__ int s_key[SF_MAX_TOPK];
+  __shared__ int s_rowid[SF_MAX_TOPK];
   __shared__ int s_row[SF_MAX_TOPK];
+  __shared__ int s_n;
   const int t = blockIdx.x;
+  if (threadIdx.x < K) {
+    const int j = threadIdx.x;
+    const int64_t e = idx[static_cast<int64_t>(t) * K + j];
+    const int r = inv_perm[static_cast<int64_t>(t) * K + j];
+    const bool ok = e >= 0 && e < E && r >= 0;
+    s_key[j] = ok ? (use_rank ? ranks.rank[e] : static_cast<int>(e)) : -1;
+    s_rowid[j] = ok ? r : -1;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    // Order this token's routes: insertion sort on (rank, position).
+    // Insertion sort on (rank, position); equal keys keep position order.
     int key[SF_MAX_TOPK];
-    int row[SF_MAX_TOPK];
     int n = 0;
     for (int j = 0; j < K; ++j) {
-      const int64_t e = idx[static_cast<int64_t>(t) * K + j];
-      const int r = inv_perm[static_cast<int64_t>(t) * K + j];
-      if (e < 0 || e >= E || r < 0) continue;
-      const int k = use_rank ? ranks.rank[e] : static_cast<int>(e);
+      if (s_rowid[j] < 0) continue;
+      const int k = s_key[j];
       int p = n++;
-      while (p > 0 && key[p - 1] > k) {  // equal keys keep position order
+      while (p > 0 && key[p - 1] > k) {
         key[p] = key[p - 1];
-        row[p] = row[p - 1];
+        s_row[p] = s_row[p - 1];
         --p;
       }
       key[p] = k;
-      row[p] = r;
+      s_row[p] = s_rowid[j];
     }
-    for (int j = 0; j < K; ++j) s_row[j] = j < n ? row[j] : -1;
+    s_n = n;
   }
   __syncthreads();
   const int c0 = blockIdx.y * kColsPerBlock + threadIdx.x * kColsPerThread;
   if (c0 >= H) return;
+  const int n = s_n;
   float acc[kColsPerThread];
 #pragma unroll
   for (int c = 0; c < kColsPerThread; ++c) acc[c] = 0.0f;
-  for (int j = 0; j < K; ++j) {
-    const int r = s_row[j];
-    if (r < 0) break;
-    const uint16_t* src = rows + static_cast<int64_t>(r) * H + c0;
-    uint16_t v[kColsPerThread];
-    if (kVec) {
-      const uint4 q = *reinterpret_cast<const uint4*>(src);
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  for (int j0 = 0; j0 < n; j0 += kPrefetch) {
+    uint16_t v[kPrefetch][kColsPerThread];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        v[2 * c] = static_cast<uint16_t>(w[c] & 0xffffu);
-        v[2 * c + 1] = static_cast<uint16_t>(w[c] >> 16);
+    for (int j = 0; j < kPrefetch; ++j) {
+      if (j0 + j < n) {
+        const uint16_t* src = rows + static_cast<int64_t>(s_row[j0 + j]) * H + c0;
+        if (kVec) {
+          unpack8(*reinterpret_cast<const uint4*>(src), v[j]);
+        } else {
+#pragma unroll
+          for (int c = 0; c < kColsPerThread; ++c) v[j][c] = c0 + c < H ? src[c] : 0;
+        }
       }
-    } else {
-#pragma unroll
-      for (int c = 0; c < kColsPerThread; ++c) v[c] = c0 + c < H ? src[c] : 0;
     }
 #pragma unroll
-    for (int c = 0; c < kColsPerThread; ++c) {
-      const float s = acc[c] + sf_bf16_to_f32(v[c]);
-      acc[c] = acc_fp32 ? s : sf_round_bf16(s);
+    for (int j = 0; j < kPrefetch; ++j) {
+      if (j0 + j < n) {
+#pragma unroll
+        for (int c = 0; c < kColsPerThread; ++c) {
+          const float s = acc[c] + sf_bf16_to_f32(v[j][c]);
+          acc[c] = acc_fp32 ? s : sf_round_bf16(s);
+        }
+      }
     }
   }
   uint16_t* dst = out + static_cast<int64_t>(t) * H + c0;

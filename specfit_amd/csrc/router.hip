@@ -129,12 +129,24 @@ __device__ void softmax_topk_wave(const float* s_logit, int E, int K, int renorm
 
 // Vector path: hidden_size % 8 == 0, 16-byte aligned rows, and at most
 // NCH chunks of 8 elements per lane, so the token's hidden row stays in
-// registers while the wavefront walks its experts.
+// registers.  Sixteen wavefronts share the experts; each takes them four at
+// a time with all router-weight loads of the four issued before any use, so
+// the block is bound by one L2 round trip per group instead of one per
+// expert.
+constexpr int kRouterVecThreads = 1024;
+constexpr int kRouterVecWaves = kRouterVecThreads / SF_WAVE;
+// Experts per group: 16 uint4 router-weight registers per lane at most.
 template <int NCH>
-__global__ __launch_bounds__(kRouterThreads) void router_topk_vec_kernel(
+struct ExpertGroup {
+  static constexpr int value = NCH <= 4 ? 4 : (NCH <= 8 ? 2 : 1);
+};
+
+template <int NCH>
+__global__ __launch_bounds__(kRouterVecThreads) void router_topk_vec_kernel(
     const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ wr, int H,
     int E, int K, int renorm, uint16_t* __restrict__ logits,
     uint16_t* __restrict__ topw, int64_t* __restrict__ topi) {
+  constexpr int kExpertGroup = ExpertGroup<NCH>::value;
   __shared__ float s_logit[SF_MAX_EXPERTS];
   __shared__ float s_val[SF_MAX_TOPK];
   __shared__ int s_id[SF_MAX_TOPK];
@@ -149,33 +161,39 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_vec_kernel(
     int c = lane + SF_WAVE * i;
     hreg[i] = c < nchunks ? h4[c] : make_uint4(0, 0, 0, 0);
   }
-  // Two experts per iteration for independent accumulation chains.
-  for (int e0 = wave * 2; e0 < E; e0 += kRouterWaves * 2) {
-    const int e1 = e0 + 1;
-    const uint4* w0 = reinterpret_cast<const uint4*>(wr + static_cast<size_t>(e0) * H);
-    const uint4* w1 = reinterpret_cast<const uint4*>(wr + static_cast<size_t>(e1 < E ? e1 : e0) * H);
-    float a0 = 0.0f, a1 = 0.0f;
+  for (int e0 = wave * kExpertGroup; e0 < E; e0 += kRouterVecWaves * kExpertGroup) {
+    uint4 wv[kExpertGroup][NCH];
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      int c = lane + SF_WAVE * i;
-      if (c < nchunks) {
-        uint4 v0 = w0[c];
-        uint4 v1 = w1[c];
-        a0 = dot8_acc(hreg[i], v0, a0);
-        a1 = dot8_acc(hreg[i], v1, a1);
+    for (int g = 0; g < kExpertGroup; ++g) {
+      const int e = min(e0 + g, E - 1);
+      const uint4* w4 = reinterpret_cast<const uint4*>(wr + static_cast<size_t>(e) * H);
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        int c = lane + SF_WAVE * i;
+        wv[g][i] = c < nchunks ? w4[c] : make_uint4(0, 0, 0, 0);
       }
     }
-    a0 = wave_sum_butterfly(a0);
-    a1 = wave_sum_butterfly(a1);
-    if (lane == 0) {
-      uint16_t b0 = sf_f32_to_bf16(a0);
-      logits[static_cast<size_t>(t) * E + e0] = b0;
-      s_logit[e0] = sf_bf16_to_f32(b0);
-      if (e1 < E) {
-        uint16_t b1 = sf_f32_to_bf16(a1);
-        logits[static_cast<size_t>(t) * E + e1] = b1;
-        s_logit[e1] = sf_bf16_to_f32(b1);
-      }
+    float acc[kExpertGroup];
+#pragma unroll
+    for (int g = 0; g < kExpertGroup; ++g) {
+      acc[g] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NCH; ++i)
+        if (lane + SF_WAVE * i < nchunks) acc[g] = dot8_acc(hreg[i], wv[g][i], acc[g]);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+#pragma unroll
+      for (int g = 0; g < kExpertGroup; ++g) acc[g] += __shfl_xor(acc[g], d, SF_WAVE);
+    }
+    if (lane < kExpertGroup && e0 + lane < E) {
+      float a = acc[0];
+#pragma unroll
+      for (int g = 1; g < kExpertGroup; ++g)
+        if (lane == g) a = acc[g];
+      const uint16_t b = sf_f32_to_bf16(a);
+      logits[static_cast<size_t>(t) * E + e0 + lane] = b;
+      s_logit[e0 + lane] = sf_bf16_to_f32(b);
     }
   }
   __syncthreads();
@@ -245,6 +263,7 @@ extern "C" int sf_router_topk(const void* hidden, const void* router_weight,
   const int per_lane = (nchunks + SF_WAVE - 1) / SF_WAVE;
   dim3 grid(tokens), block(kRouterThreads);
   if (aligned && per_lane <= 16) {
+    block = dim3(kRouterVecThreads);
     if (per_lane <= 1)
       router_topk_vec_kernel<1><<<grid, block, 0, s>>>(h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
     else if (per_lane <= 2)

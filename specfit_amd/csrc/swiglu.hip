@@ -6,18 +6,33 @@
 // with GU = packed[0:2IH] as [2I, H] and D = packed[2IH:] as [H, I].
 //
 // At verification sizes an expert sees m <= a few dozen rows, so each weight
-// element is used m times: the GEMMs are bound by streaming the 9 MiB of
-// expert weights from HBM.  Both phases therefore stream every weight byte
-// exactly once straight into MFMA operand registers (16-byte loads, no LDS
-// round trip), with the token rows (a few KiB, L2 resident) as the other
-// operand.
+// element is used m times and the GEMMs are bound by streaming the 9 MiB of
+// expert weights from HBM.  Every weight byte is read exactly once.
+//
+// Weight access pattern.  A 16x16x32 MFMA B operand, loaded directly, touches
+// 16 weight rows x 64 B per load instruction; on MI355X that pattern streams
+// HBM at ~4.4 TB/s, while row-contiguous 1 KiB loads stream at ~6.2 TB/s.  So
+// weights are read as blocks of 2 rows x 512 B per instruction (256 k per
+// row), written to a wavefront-private, row-padded LDS tile (16 B of padding
+// per row keeps the transposed reads free of bank conflicts) and read back in
+// MFMA-operand order.  Token rows (the A operand, a few KiB, L2 resident) are
+// loaded straight into registers.
 //
 // Phase 1 (gate/up): a workgroup owns 16 activation columns of one expert,
-// i.e. 16 gate rows + 16 up rows of GU (2 x 16 x H bf16).  Its 4 wavefronts
-// split H into quarters; partial tiles are summed in LDS in wavefront order
+// i.e. 16 gate rows + 16 up rows of GU.  Its 4 wavefronts split H into
+// quarters; partial tiles are summed in LDS in wavefront order
 // (deterministic), then the SwiGLU epilogue writes bf16 activations.
 // Phase 2 (down): a workgroup owns 64 output columns (4 wavefronts x 16) of
-// one expert over the full I, the epilogue applies the routing weight.
+// one expert over the full I; the epilogue applies the routing weight.
+//
+// Rows per pass: each workgroup picks 1, 2 or 4 sixteen-row MFMA tiles from
+// its own expert's row count (capped by the launch's max_rows), so small
+// experts do not pay for the largest expert of a launch.  Rows past the end
+// of a pass repeat the pass's last row: an MFMA output row depends only on
+// its own A row and rows past the end are never stored, so the loads need
+// no per-lane branches.  The fp32 summation order of every output is fixed
+// by (H, I) alone, so results do not depend on grouping, tile count or
+// launch.
 // MFMA: v_mfma_f32_16x16x32_bf16, A = token rows (M), B = weight rows (N).
 #include "sf_common.h"
 
@@ -26,12 +41,10 @@ namespace {
 constexpr int kMaxListExperts = 128;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / SF_WAVE;
-constexpr int kMTiles = 4;             // 16-row MFMA tiles per pass (64 rows)
-constexpr int kPassRows = 16 * kMTiles;
 constexpr int kGateCols = 16;          // activation columns per phase-1 workgroup
 constexpr int kDownCols = 16 * kWaves; // output columns per phase-2 workgroup
-constexpr int kUnroll1 = 4;
-constexpr int kUnroll2 = 8;
+constexpr int kBlockK = 256;           // k per staged weight block
+constexpr int kRowBytes = kBlockK * 2 + 16;  // padded LDS row (bytes)
 
 enum class Resolve { kList, kTable, kDense };
 
@@ -103,74 +116,95 @@ __device__ __forceinline__ sf_f32x4 mfma16(uint4 a, uint4 b, sf_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
+// Stage ROWS (even) weight rows x kBlockK k into a wavefront's LDS tile:
+// lane l loads 16 B of row 2i + l/32 at k offset 8*(l%32); row r of the
+// block starts at w_row0 + r * row_stride.
+template <int ROWS>
+__device__ __forceinline__ void stage_block(const uint16_t* w_row0, int64_t row_stride,
+                                            char* tile, int lane) {
+  const int half = lane >> 5;
+  const int col = (lane & 31) * 8;
+  uint4 v[ROWS / 2];
+#pragma unroll
+  for (int i = 0; i < ROWS / 2; ++i)
+    v[i] = ld16(w_row0 + static_cast<int64_t>(2 * i + half) * row_stride + col);
+#pragma unroll
+  for (int i = 0; i < ROWS / 2; ++i)
+    *reinterpret_cast<uint4*>(tile + (2 * i + half) * kRowBytes + col * 2) = v[i];
+}
+
+// MFMA B fragment of k-step s (32 k) for tile rows [r0, r0 + 16): lane l
+// takes row r0 + l%16, k 8*(l/16) .. +7 of the step.
+__device__ __forceinline__ uint4 frag_b(const char* tile, int r0, int s, int lane) {
+  return *reinterpret_cast<const uint4*>(tile + (r0 + (lane & 15)) * kRowBytes + s * 64 +
+                                         (lane >> 4) * 16);
+}
+
+// Sixteen-row tiles needed by an expert of m rows, capped at MTMAX.
+template <int MTMAX>
+__device__ __forceinline__ int tiles_for(int m) {
+  return (min(m, 16 * MTMAX) + 15) / 16;
+}
+
 // ---------------------------------------------------------------- phase 1 --
-template <Resolve R>
-__global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const SwigluArgs a) {
-  __shared__ float s_part[kWaves][2][kPassRows][kGateCols];
-  const int tiles = a.I / kGateCols;
-  const int j = blockIdx.x / tiles;
-  const int tile = blockIdx.x - j * tiles;
-  ExpertWork wk;
-  if (!resolve<R>(a, j, wk)) return;
+template <Resolve R, int MT>
+__device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWork& wk, int tile,
+                                            char* smem) {
+  constexpr int kRows = 16 * MT;
+  auto s_part = reinterpret_cast<float(*)[2][kRows][kGateCols]>(smem);
+  auto s_w = reinterpret_cast<char(*)[32 * kRowBytes]>(smem);
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int H = a.H;
   const int c0 = tile * kGateCols;
-  const int kq = H / kWaves;  // this wavefront's K range
+  const int kq = H / kWaves;
   const int kbeg = wave * kq;
   const int lrow = lane & 15;
   const int kl = 8 * (lane >> 4);
-  const uint16_t* wg = wk.w + static_cast<int64_t>(c0 + lrow) * H + kbeg + kl;
-  const uint16_t* wu = wk.w + static_cast<int64_t>(a.I + c0 + lrow) * H + kbeg + kl;
-  const int steps = kq / 32;
+  char* wt = s_w[wave];
+  // LDS tile rows 0..15: gate rows c0.., rows 16..31: up rows I + c0..
+  const uint16_t* wgate = wk.w + static_cast<int64_t>(c0) * H + kbeg;
+  const uint16_t* wup = wk.w + static_cast<int64_t>(a.I + c0) * H + kbeg;
+  const int blocks = kq / kBlockK;
 
-  for (int p0 = 0; p0 < wk.m; p0 += kPassRows) {
-    const int mp = min(kPassRows, wk.m - p0);
-    const int mt_live = (mp + 15) / 16;
-    const uint16_t* xr[kMTiles];
+  for (int p0 = 0; p0 < wk.m; p0 += kRows) {
+    const int mp = min(kRows, wk.m - p0);
+    const uint16_t* xr[MT];
 #pragma unroll
-    for (int mt = 0; mt < kMTiles; ++mt) {
-      const int row = mt * 16 + lrow;
-      xr[mt] = row < mp ? row_ptr<R>(a, wk.r0 + p0 + row) + kbeg + kl : nullptr;
-    }
-    sf_f32x4 acc[kMTiles][2];
+    for (int mt = 0; mt < MT; ++mt)
+      xr[mt] = row_ptr<R>(a, wk.r0 + p0 + min(mt * 16 + lrow, mp - 1)) + kbeg + kl;
+    sf_f32x4 acc[MT][2];
 #pragma unroll
-    for (int mt = 0; mt < kMTiles; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       acc[mt][0] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
       acc[mt][1] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    for (int s = 0; s < steps; s += kUnroll1) {
-      uint4 bg[kUnroll1], bu[kUnroll1];
+    for (int b = 0; b < blocks; ++b) {
+      stage_block<16>(wgate + b * kBlockK, H, wt, lane);
+      stage_block<16>(wup + b * kBlockK, H, wt + 16 * kRowBytes, lane);
 #pragma unroll
-      for (int u = 0; u < kUnroll1; ++u) {
-        bg[u] = ld16(wg + (s + u) * 32);
-        bu[u] = ld16(wu + (s + u) * 32);
-      }
+      for (int s = 0; s < kBlockK / 32; ++s) {
+        uint4 x[MT];
 #pragma unroll
-      for (int mt = 0; mt < kMTiles; ++mt) {
-        if (mt < mt_live) {
-          uint4 xa[kUnroll1];
+        for (int mt = 0; mt < MT; ++mt) x[mt] = ld16(xr[mt] + b * kBlockK + s * 32);
+        const uint4 g = frag_b(wt, 0, s, lane);
+        const uint4 u = frag_b(wt, 16, s, lane);
 #pragma unroll
-          for (int u = 0; u < kUnroll1; ++u)
-            xa[u] = xr[mt] ? ld16(xr[mt] + (s + u) * 32) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-          for (int u = 0; u < kUnroll1; ++u) {
-            acc[mt][0] = mfma16(xa[u], bg[u], acc[mt][0]);
-            acc[mt][1] = mfma16(xa[u], bu[u], acc[mt][1]);
-          }
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt][0] = mfma16(x[mt], g, acc[mt][0]);
+          acc[mt][1] = mfma16(x[mt], u, acc[mt][1]);
         }
       }
     }
+    __syncthreads();  // every wavefront is done with its weight tile
     // D layout: lane holds rows 4*(lane/16)+i, column lane%16.
 #pragma unroll
-    for (int mt = 0; mt < kMTiles; ++mt) {
-      if (mt < mt_live) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = mt * 16 + 4 * (lane >> 4) + i;
-          s_part[wave][0][row][lrow] = acc[mt][0][i];
-          s_part[wave][1][row][lrow] = acc[mt][1][i];
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int row = mt * 16 + 4 * (lane >> 4) + i;
+        s_part[wave][0][row][lrow] = acc[mt][0][i];
+        s_part[wave][1][row][lrow] = acc[mt][1][i];
       }
     }
     __syncthreads();
@@ -193,79 +227,95 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const SwigluArgs 
   }
 }
 
-// ---------------------------------------------------------------- phase 2 --
-template <Resolve R>
-__global__ __launch_bounds__(kThreads) void down_mfma_kernel(const SwigluArgs a) {
-  const int tiles = a.H / kDownCols;
+template <Resolve R, int MTMAX>
+__global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const SwigluArgs a) {
+  // The weight tiles are dead once the K loop ends, so the cross-wavefront
+  // partial sums reuse their LDS.
+  constexpr int kTileBytes = kWaves * 32 * kRowBytes;
+  constexpr int kPartBytes = kWaves * 2 * 16 * MTMAX * kGateCols * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kTileBytes > kPartBytes ? kTileBytes : kPartBytes];
+  const int tiles = a.I / kGateCols;
   const int j = blockIdx.x / tiles;
   const int tile = blockIdx.x - j * tiles;
   ExpertWork wk;
   if (!resolve<R>(a, j, wk)) return;
+  const int need = tiles_for<MTMAX>(wk.m);
+  if (MTMAX >= 4 && need > 2)
+    gateup_body<R, 4>(a, wk, tile, smem);
+  else if (MTMAX >= 2 && need > 1)
+    gateup_body<R, 2>(a, wk, tile, smem);
+  else
+    gateup_body<R, 1>(a, wk, tile, smem);
+}
+
+// ---------------------------------------------------------------- phase 2 --
+template <Resolve R, int MT>
+__device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork& wk, int tile,
+                                          char* smem) {
+  constexpr int kRows = 16 * MT;
+  auto s_w = reinterpret_cast<char(*)[16 * kRowBytes]>(smem);
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int I = a.I;
   const int n0 = tile * kDownCols + wave * 16;
   const int lrow = lane & 15;
   const int kl = 8 * (lane >> 4);
-  const uint16_t* wd = wk.w + 2 * static_cast<int64_t>(a.I) * a.H +
-                       static_cast<int64_t>(n0 + lrow) * I + kl;
-  const int steps = I / 32;
+  char* wt = s_w[wave];
+  const uint16_t* wd = wk.w + 2 * static_cast<int64_t>(a.I) * a.H + static_cast<int64_t>(n0) * I;
+  const int blocks = I / kBlockK;
 
-  for (int p0 = 0; p0 < wk.m; p0 += kPassRows) {
-    const int mp = min(kPassRows, wk.m - p0);
-    const int mt_live = (mp + 15) / 16;
-    sf_f32x4 acc[kMTiles];
+  for (int p0 = 0; p0 < wk.m; p0 += kRows) {
+    const int mp = min(kRows, wk.m - p0);
+    const uint16_t* ar[MT];
 #pragma unroll
-    for (int mt = 0; mt < kMTiles; ++mt) acc[mt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint16_t* ar[kMTiles];
+    for (int mt = 0; mt < MT; ++mt)
+      ar[mt] = a.act + static_cast<int64_t>(wk.r0 + p0 + min(mt * 16 + lrow, mp - 1)) * I + kl;
+    sf_f32x4 acc[MT];
 #pragma unroll
-    for (int mt = 0; mt < kMTiles; ++mt) {
-      const int row = mt * 16 + lrow;
-      ar[mt] = row < mp ? a.act + static_cast<int64_t>(wk.r0 + p0 + row) * I + kl : nullptr;
-    }
-    int s = 0;
-    for (; s + kUnroll2 <= steps; s += kUnroll2) {
-      uint4 b[kUnroll2];
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < blocks; ++b) {
+      stage_block<16>(wd + b * kBlockK, I, wt, lane);
 #pragma unroll
-      for (int u = 0; u < kUnroll2; ++u) b[u] = ld16(wd + (s + u) * 32);
+      for (int s = 0; s < kBlockK / 32; ++s) {
+        uint4 x[MT];
 #pragma unroll
-      for (int mt = 0; mt < kMTiles; ++mt) {
-        if (mt < mt_live) {
-          uint4 xa[kUnroll2];
+        for (int mt = 0; mt < MT; ++mt) x[mt] = ld16(ar[mt] + b * kBlockK + s * 32);
+        const uint4 d = frag_b(wt, 0, s, lane);
 #pragma unroll
-          for (int u = 0; u < kUnroll2; ++u)
-            xa[u] = ar[mt] ? ld16(ar[mt] + (s + u) * 32) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-          for (int u = 0; u < kUnroll2; ++u) acc[mt] = mfma16(xa[u], b[u], acc[mt]);
-        }
-      }
-    }
-    for (; s < steps; ++s) {
-      const uint4 b = ld16(wd + s * 32);
-#pragma unroll
-      for (int mt = 0; mt < kMTiles; ++mt) {
-        if (mt < mt_live) {
-          const uint4 xa = ar[mt] ? ld16(ar[mt] + s * 32) : make_uint4(0, 0, 0, 0);
-          acc[mt] = mfma16(xa, b, acc[mt]);
-        }
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16(x[mt], d, acc[mt]);
       }
     }
 #pragma unroll
-    for (int mt = 0; mt < kMTiles; ++mt) {
-      if (mt < mt_live) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = mt * 16 + 4 * (lane >> 4) + i;
-          if (row < mp) {
-            const int r = wk.r0 + p0 + row;
-            float y = sf_round_bf16(acc[mt][i]);
-            if (a.route_w) y = y * sf_bf16_to_f32(a.route_w[a.perm_pos[r]]);
-            a.out[static_cast<int64_t>(r) * a.H + n0 + lrow] = sf_f32_to_bf16(y);
-          }
+      for (int i = 0; i < 4; ++i) {
+        const int row = mt * 16 + 4 * (lane >> 4) + i;
+        if (row < mp) {
+          const int r = wk.r0 + p0 + row;
+          float y = sf_round_bf16(acc[mt][i]);
+          if (a.route_w) y = y * sf_bf16_to_f32(a.route_w[a.perm_pos[r]]);
+          a.out[static_cast<int64_t>(r) * a.H + n0 + lrow] = sf_f32_to_bf16(y);
         }
       }
     }
   }
+}
+
+template <Resolve R, int MTMAX>
+__global__ __launch_bounds__(kThreads) void down_mfma_kernel(const SwigluArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kWaves * 16 * kRowBytes];
+  const int tiles = a.H / kDownCols;
+  const int j = blockIdx.x / tiles;
+  const int tile = blockIdx.x - j * tiles;
+  ExpertWork wk;
+  if (!resolve<R>(a, j, wk)) return;
+  const int need = tiles_for<MTMAX>(wk.m);
+  if (MTMAX >= 4 && need > 2)
+    down_body<R, 4>(a, wk, tile, smem);
+  else if (MTMAX >= 2 && need > 1)
+    down_body<R, 2>(a, wk, tile, smem);
+  else
+    down_body<R, 1>(a, wk, tile, smem);
 }
 
 // ------------------------------------------------ generic (any shape) path --
@@ -319,27 +369,38 @@ __global__ __launch_bounds__(kThreads) void down_generic_kernel(const SwigluArgs
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool mfma_shape_ok(int H, int I) {
-  return H % (kWaves * 32 * kUnroll1) == 0 && H % kDownCols == 0 &&
-         I % kGateCols == 0 && I % 32 == 0;
+  // phase 1: each wavefront's K range (H/4) is whole staged blocks; phase 2:
+  // I is whole staged blocks and H whole 64-column workgroups.
+  return H % (kWaves * kBlockK) == 0 && H % kDownCols == 0 && I % kGateCols == 0 &&
+         I % kBlockK == 0;
 }
 
+template <Resolve R, int MTMAX>
+int launch_mfma(const SwigluArgs& a, long long g1, long long g2, hipStream_t s) {
+  gateup_mfma_kernel<R, MTMAX><<<dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, s>>>(a);
+  SF_LAUNCH_CHECK();
+  down_mfma_kernel<R, MTMAX><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
+  SF_LAUNCH_CHECK();
+  return SF_OK;
+}
+
+// max_rows bounds the rows of any expert of the launch; it only caps the
+// tile count (results do not depend on it).
 template <Resolve R>
-int launch(const SwigluArgs& a, int groups, bool mfma, hipStream_t s) {
+int launch(const SwigluArgs& a, int groups, bool mfma, int max_rows, hipStream_t s) {
   if (groups <= 0) return SF_OK;
   if (mfma) {
     const long long g1 = static_cast<long long>(groups) * (a.I / kGateCols);
     const long long g2 = static_cast<long long>(groups) * (a.H / kDownCols);
     if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
-    gateup_mfma_kernel<R><<<dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, s>>>(a);
-    SF_LAUNCH_CHECK();
-    down_mfma_kernel<R><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
-    SF_LAUNCH_CHECK();
-  } else {
-    gateup_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
-    SF_LAUNCH_CHECK();
-    down_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
-    SF_LAUNCH_CHECK();
+    if (max_rows <= 16) return launch_mfma<R, 1>(a, g1, g2, s);
+    if (max_rows <= 32) return launch_mfma<R, 2>(a, g1, g2, s);
+    return launch_mfma<R, 4>(a, g1, g2, s);
   }
+  gateup_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
+  SF_LAUNCH_CHECK();
+  down_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
+  SF_LAUNCH_CHECK();
   return SF_OK;
 }
 
@@ -354,14 +415,14 @@ int check_common(int tokens, int top_k, int H, int I) {
 extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
                                  const int32_t* offsets, const void* route_weights,
                                  int tokens, int top_k, int hidden_size,
-                                 int intermediate_size, int n_experts,
+                                 int intermediate_size, int n_experts, int max_rows,
                                  const int32_t* expert_ids,
                                  const uint64_t* expert_weights,
                                  void* act_workspace, void* out_rows,
                                  sf_stream_t stream) {
   int rc = check_common(tokens, top_k, hidden_size, intermediate_size);
   if (rc) return rc;
-  if (n_experts < 0) return SF_ERR_INVALID_ARGUMENT;
+  if (n_experts < 0 || max_rows < 1) return SF_ERR_INVALID_ARGUMENT;
   if (n_experts == 0 || tokens == 0) return SF_OK;
   if (!hidden || !perm_pos || !offsets || !expert_ids || !expert_weights ||
       !act_workspace || !out_rows)
@@ -390,7 +451,7 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
       a.expert[i] = expert_ids[base + i];
       a.wptr[i] = expert_weights[base + i];
     }
-    rc = launch<Resolve::kList>(a, a.n, mfma, s);
+    rc = launch<Resolve::kList>(a, a.n, mfma, max_rows, s);
     if (rc) return rc;
   }
   return SF_OK;
@@ -429,7 +490,8 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
   a.slot_of_expert = slot_of_expert;
   a.slot_base = static_cast<const uint16_t*>(slot_base);
   a.slot_stride = slot_stride_elems;
-  return launch<Resolve::kTable>(a, num_experts, mfma, reinterpret_cast<hipStream_t>(stream));
+  return launch<Resolve::kTable>(a, num_experts, mfma, tokens * top_k,
+                                 reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int sf_expert_swiglu(const void* rows, int m, int64_t row_stride,
@@ -454,5 +516,5 @@ extern "C" int sf_expert_swiglu(const void* rows, int m, int64_t row_stride,
   a.dense_m = m;
   a.n = 1;
   a.wptr[0] = reinterpret_cast<uint64_t>(packed_weights);
-  return launch<Resolve::kDense>(a, 1, mfma, reinterpret_cast<hipStream_t>(stream));
+  return launch<Resolve::kDense>(a, 1, mfma, m, reinterpret_cast<hipStream_t>(stream));
 }

@@ -244,9 +244,13 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
     if rec is not None:
         s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
         start, end = rec._events(s)
+    max_rows = N
+    if plan.host_counts is not None:
+        counts = plan.host_counts[0]
+        max_rows = max(1, max(int(counts[int(e)]) for e in expert_ids))
     rc = _native.lib().sf_grouped_swiglu(
         _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
-        plan.tokens, plan.top_k, hidden_size, intermediate_size, n,
+        plan.tokens, plan.top_k, hidden_size, intermediate_size, n, max_rows,
         ctypes.cast(id_arr, ctypes.c_void_p), ctypes.cast(w_arr, ctypes.c_void_p),
         _ptr(act), _ptr(out_rows), _stream_handle(stream, hidden.device))
     _native.check(rc, "sf_grouped_swiglu")
@@ -254,7 +258,6 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
         end.record(s)
         rows = 0
         if plan.host_counts is not None:
-            counts = plan.host_counts[0]
             rows = int(sum(int(counts[int(e)]) for e in expert_ids))
         rec.k3.append((n, rows, tag, start, end))
 
