@@ -154,24 +154,35 @@ class DispatchPlan:
     tokens: int
     top_k: int
     num_experts: int
-    counts: torch.Tensor
-    offsets: torch.Tensor
+    meta: torch.Tensor            # int32 [2, E+1]: row 0 counts, row 1 offsets
     perm_pos: torch.Tensor
     inv_perm: torch.Tensor
     host_counts: torch.Tensor | None = None
-    ready: torch.cuda.Event | None = None
 
-    def fetch_counts(self) -> torch.Tensor:
-        """Copy counts+offsets to pinned host memory and wait for them."""
+    @property
+    def counts(self) -> torch.Tensor:
+        return self.meta[0]
+
+    @property
+    def offsets(self) -> torch.Tensor:
+        return self.meta[1]
+
+    def fetch_counts(self, staging: torch.Tensor | None = None) -> torch.Tensor:
+        """Copy [counts; offsets] to pinned host memory in one transfer and
+        wait for it.  ``staging`` is a reusable pinned int32 [2, E+1] buffer;
+        without one a pinned buffer is allocated (which may synchronise the
+        device while the allocator grows, so hot paths pass one)."""
         if self.host_counts is None:
-            pinned = torch.empty((2, self.num_experts + 1), dtype=torch.int32,
-                                 pin_memory=True)
-            pinned[0].copy_(self.counts, non_blocking=True)
-            pinned[1].copy_(self.offsets, non_blocking=True)
+            shape = (2, self.num_experts + 1)
+            if staging is None:
+                staging = torch.empty(shape, dtype=torch.int32, pin_memory=True)
+            elif staging.shape != shape or staging.dtype != torch.int32 or not staging.is_pinned():
+                raise ValueError("staging must be pinned int32 [2, num_experts + 1]")
+            staging.copy_(self.meta, non_blocking=True)
             ev = torch.cuda.Event()
-            ev.record(torch.cuda.current_stream(self.counts.device))
+            ev.record(torch.cuda.current_stream(self.meta.device))
             ev.synchronize()
-            self.host_counts = pinned
+            self.host_counts = staging
         return self.host_counts
 
     def active_experts(self) -> tuple[int, ...]:
@@ -193,19 +204,17 @@ def dispatch(index: torch.Tensor, num_experts: int, *,
     index = index.contiguous()
     T, K = index.shape
     dev = index.device
-    counts = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
-    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    meta = torch.empty((2, num_experts + 1), dtype=torch.int32, device=dev)
     perm = torch.empty(T * K, dtype=torch.int32, device=dev)
     inv = torch.empty(T * K, dtype=torch.int32, device=dev)
     if T * K == 0:
-        counts.zero_()
-        offsets.zero_()
-        return DispatchPlan(T, K, int(num_experts), counts, offsets, perm, inv)
-    rc = _native.lib().sf_dispatch(_ptr(index), T, K, int(num_experts), _ptr(counts),
-                                   _ptr(offsets), _ptr(perm), _ptr(inv),
+        meta.zero_()
+        return DispatchPlan(T, K, int(num_experts), meta, perm, inv)
+    rc = _native.lib().sf_dispatch(_ptr(index), T, K, int(num_experts), _ptr(meta[0]),
+                                   _ptr(meta[1]), _ptr(perm), _ptr(inv),
                                    _stream_handle(stream, dev))
     _native.check(rc, "sf_dispatch")
-    return DispatchPlan(T, K, int(num_experts), counts, offsets, perm, inv)
+    return DispatchPlan(T, K, int(num_experts), meta, perm, inv)
 
 
 # ------------------------------------------------------------------ K3 ----

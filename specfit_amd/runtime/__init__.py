@@ -8,6 +8,9 @@ from .gpu_expert_cache import GpuExpertCache
 from .lease import ExpertCacheStats, ExpertLease, NoEvictableSlotError
 from .qwen3_offloaded_experts import (ExpertExecutionPolicy, Qwen3OffloadedExperts,
                                       ReductionMode)
+from .qwen3_expert_prefetch import Qwen3ExpertPrefetch
+from .qwen3_offloaded_model import (LoadedOffloadedQwen3, Qwen3LoadTimings, build_offloaded_qwen3,
+                                    load_offloaded_qwen3)
 from .qwen3_router import Qwen3MoeTopKRouterHip
 from .state import ExpertKey
 from .trace import RuntimeEventKind
@@ -16,7 +19,9 @@ __all__ = [
     "CacheSlotSnapshot", "CacheTransition", "CacheTransitionCounters",
     "CacheTransitionObserver", "ExpertCacheStats", "ExpertExecutionPolicy", "ExpertKey",
     "ExpertLease", "GpuExpertCache", "GpuExpertCacheSnapshot", "NoEvictableSlotError",
-    "PendingTransferSnapshot", "Qwen3MoeTopKRouterHip", "Qwen3OffloadedExperts",
+    "LoadedOffloadedQwen3", "PendingTransferSnapshot", "Qwen3ExpertPrefetch", "Qwen3LoadTimings",
+    "Qwen3MoeTopKRouterHip", "Qwen3OffloadedExperts", "build_offloaded_qwen3",
+    "load_offloaded_qwen3",
     "RecordingCacheTransitionObserver", "ReductionMode", "RuntimeEventKind",
     "aggregate_cache_transition_counters",
 ]

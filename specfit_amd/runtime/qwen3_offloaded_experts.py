@@ -136,6 +136,9 @@ class Qwen3OffloadedExperts(nn.Module):
         self.combine_fp32 = combine_fp32
         self._prediction_scheduler = None
         self._num_experts: int | None = None
+        # Reused pinned staging of the per-forward [counts; offsets] read
+        # (allocated once: growing the pinned pool can synchronise the device).
+        self._host_counts: torch.Tensor | None = None
 
     # -------------------------------------------------------------- forward --
     def forward(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
@@ -206,7 +209,10 @@ class Qwen3OffloadedExperts(nn.Module):
             return None, ()
         num_experts = self.num_experts()
         plan = _dispatch(top_k_index, num_experts)
-        counts = plan.fetch_counts()[0]
+        if self._host_counts is None:
+            self._host_counts = torch.empty((2, num_experts + 1), dtype=torch.int32,
+                                            pin_memory=True)
+        counts = plan.fetch_counts(self._host_counts)[0]
         if int(counts[num_experts]):
             self._raise_invalid_index(top_k_index, num_experts)
         active = tuple(int(e) for e in torch.nonzero(counts[:num_experts]).flatten().tolist())

@@ -1,0 +1,445 @@
+"""Predicted-prefetch scheduler and offloaded model loader on the device.
+
+Restates the reference's scheduler tests
+(tests/gpu/test_qwen3_expert_prefetch.py:77-440) and loader tests
+(tests/gpu/test_qwen3_offloaded_model.py:154-272) for this runtime.  Where
+the reference compares the offloaded model with HF eager bitwise (same
+cuBLAS kernels), this build compares within the MoE tolerance: its expert
+GEMMs and combine are different kernels.
+"""
+import json
+import tempfile
+from contextlib import ExitStack
+from pathlib import Path
+from types import MappingProxyType, SimpleNamespace
+from unittest.mock import patch
+
+import pytest
+import torch
+from torch import nn
+
+from specfit_amd.runtime import (ExpertKey, GpuExpertCache, LoadedOffloadedQwen3,
+                                 Qwen3OffloadedExperts, RecordingCacheTransitionObserver,
+                                 RuntimeEventKind, load_offloaded_qwen3)
+from specfit_amd.runtime import qwen3_offloaded_experts as implementation
+
+pytestmark = pytest.mark.gpu
+
+
+class _Attention(nn.Module):
+    def forward(self, hidden):
+        return hidden.clone()
+
+
+class _Model(nn.Module):
+    def __init__(self, experts):
+        super().__init__()
+        self.model = nn.Module()
+        self.model.layers = nn.ModuleList()
+        self.config = SimpleNamespace(num_hidden_layers=len(experts))
+        for module in experts:
+            layer = nn.Module()
+            layer.self_attn = _Attention()
+            layer.mlp = nn.Module()
+            layer.mlp.experts = module
+            self.model.layers.append(layer)
+
+    def forward(self, hidden, indices, weights):
+        for layer in self.model.layers:
+            hidden = layer.self_attn(hidden)
+            hidden = layer.mlp.experts(hidden, indices, weights)
+        return hidden
+
+
+def _case(slots=3, layers=2):
+    g = torch.Generator().manual_seed(909)
+    caches, experts = [], []
+    observer = RecordingCacheTransitionObserver(run_id="predicted-prefetch")
+    for lid in range(layers):
+        sources = {ExpertKey(lid, e): torch.randn(3 * 16 * 12, generator=g, dtype=torch.bfloat16) / 16
+                   for e in range(6)}
+        cache = GpuExpertCache(sources, slot_count=slots, device="cuda:0",
+                               cache_id=f"qwen3-layer-{lid}", queue_id=f"layer-{lid}-copy",
+                               observer=observer)
+        caches.append(cache)
+        experts.append(Qwen3OffloadedExperts(layer_id=lid, cache=cache, hidden_size=16,
+                                             intermediate_size=12, h2d_prefetch=False))
+    loaded = LoadedOffloadedQwen3(_Model(experts), tuple(caches), None)
+    inputs = (torch.randn(4, 16, generator=g, dtype=torch.bfloat16).cuda(),
+              torch.tensor([[4, 0, 2], [1, 4, 3], [2, 0, 1], [4, 3, 0]], device="cuda:0"),
+              torch.rand(4, 3, generator=g, dtype=torch.bfloat16).cuda())
+    return loaded, observer, inputs
+
+
+def _assert_restored(loaded, streams):
+    torch.cuda.synchronize()
+    for layer, cache, stream in zip(loaded.model.model.layers, loaded.expert_caches, streams):
+        assert cache.copy_stream is stream
+        assert layer.mlp.experts._prediction_scheduler is None
+        snap = cache.snapshot()
+        assert not snap.pending_transfers
+        assert all(not s.active_leases and not s.pending_use_guards for s in snap.slots)
+
+
+def _close(loaded):
+    torch.cuda.synchronize()
+    loaded.close()
+
+
+def test_bitwise_outputs_with_correct_missing_wrong_and_duplicate_predictions(device):
+    for slots in (1, 2, 3, 6):
+        loaded, _, inputs = _case(slots)
+        expected = loaded.model(*inputs)
+        streams = tuple(c.copy_stream for c in loaded.expert_caches)
+        for prediction in ((), (0, 1, 2, 3, 4), (5,), (4, 0, 4, 2, 5)):
+            for depth in (0, 1):
+                loaded.cold_reset_expert_caches()
+                with loaded.prefetch_experts({i: prediction for i in range(2)},
+                                             lookahead_layers=depth, max_inflight=2) as sched:
+                    actual = loaded.model(*inputs)
+                assert torch.equal(actual, expected), (slots, prediction, depth)
+                _assert_restored(loaded, streams)
+                st = sched.stats()
+                assert st["complete"] and st["peak_inflight"] <= 2
+                for lid, row in enumerate(st["layers"]):
+                    assert row["computed_experts"] == 5 and row["actual_experts"] == 5
+                    assert row["ready_at_router"] + row["inflight_at_router"] + row["missing_at_router"] == 5
+                    assert (row["prediction_copies"] + row["demand_copies"]
+                            == loaded.expert_caches[lid].stats().h2d_submissions)
+        _close(loaded)
+
+
+def test_grouped_routes_noncontiguous_repeated_and_empty(device):
+    for tokens in (0, 1, 4):
+        for slots in (1, 6):
+            loaded, _, (hidden, indices, weights) = _case(slots)
+            indices[0, 2] = indices[0, 0]
+            inputs = tuple(t[:tokens].t().contiguous().t() for t in (hidden, indices, weights))
+            originals = tuple(t.clone() for t in inputs)
+            expected = loaded.model(*inputs)
+            streams = tuple(c.copy_stream for c in loaded.expert_caches)
+            for depth in (0, 1):
+                loaded.cold_reset_expert_caches()
+                with loaded.prefetch_experts({0: (0, 4, 5), 1: (0, 4, 5)}, lookahead_layers=depth,
+                                             max_inflight=2):
+                    actual = loaded.model(*inputs)
+                assert torch.equal(actual, expected)
+                for a, b in zip(inputs, originals):
+                    assert torch.equal(a, b)
+                _assert_restored(loaded, streams)
+            _close(loaded)
+
+
+def test_real_misses_start_before_ready_experts_and_ready_work_precedes_wait(device):
+    loaded, _, inputs = _case(slots=4, layers=1)
+    cache = loaded.expert_caches[0]
+    # One untraced forward first so first-use work (code-object loads, pinned
+    # staging allocation) cannot synchronise the device inside the window
+    # that the sleep below holds the copy stream for.
+    loaded.model(*inputs)
+    loaded.cold_reset_expert_caches()
+    for e in (3, 4):
+        with cache.acquire(ExpertKey(0, e)) as lease:
+            lease.wait()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(cache.copy_stream):
+        torch.cuda._sleep(200_000_000)
+    with loaded.prefetch_experts({}, trace=True) as sched:
+        loaded.model(*inputs)
+    events = sched.events()
+    copies = [e for e in events if e["action"] == "copy"]
+    computed = [e for e in events if e["action"] == "compute"]
+    assert copies[0]["sequence"] < computed[0]["sequence"]
+    assert [e["expert_id"] for e in computed[:2]] == [3, 4]
+    assert all(not e["waited"] for e in computed[:2])
+    assert {e["expert_id"] for e in computed} == set(range(5))
+    _close(loaded)
+
+
+def test_predictions_are_normalised_snapshotted_and_not_truncated(device):
+    loaded, _, inputs = _case(slots=3)
+    expected = loaded.model(*inputs)
+    streams = tuple(c.copy_stream for c in loaded.expert_caches)
+    loaded.cold_reset_expert_caches()
+    predictions = {layer: [4, 0, 4, 2, 1, 3] for layer in range(2)}
+    sched = loaded.prefetch_experts(MappingProxyType(predictions), lookahead_layers=0, trace=True)
+    assert sched.predictions == ((0, 1, 2, 3, 4),) * 2
+    for ids in predictions.values():
+        ids[:] = [5]
+    with sched:
+        assert [r["expert_id"] for r in sched.events() if r["action"] == "copy"] == [0, 1]
+        actual = loaded.model(*inputs)
+    assert torch.equal(actual, expected)
+    _assert_restored(loaded, streams)
+    _close(loaded)
+
+
+def test_resident_only_forward_makes_no_copies(device):
+    loaded, _, inputs = _case(slots=6)
+    expected = loaded.model(*inputs)
+    torch.cuda.synchronize()
+    for cache in loaded.expert_caches:
+        assert len(cache.resident_expert_ids()) == 5
+    before = [c.stats().h2d_submissions for c in loaded.expert_caches]
+    queries = []
+    original = torch.cuda.Event.query
+
+    def query(event):
+        queries.append(event)
+        return original(event)
+
+    with patch.object(torch.cuda.Event, "query", query):
+        with loaded.prefetch_experts({0: tuple(range(5)), 1: tuple(range(5))}) as sched:
+            actual = loaded.model(*inputs)
+    torch.cuda.synchronize()
+    assert torch.equal(actual, expected)
+    assert len(queries) <= 10
+    assert [c.stats().h2d_submissions for c in loaded.expert_caches] == before
+    assert [r["ready_at_router"] for r in sched.stats()["layers"]] == [5, 5]
+    _close(loaded)
+
+
+def test_nonblocking_prefetch_takes_first_writable_lru_slot(device):
+    loaded, _, _ = _case(slots=4, layers=1)
+    cache = loaded.expert_caches[0]
+    for e in range(4):
+        with cache.acquire(ExpertKey(0, e)) as lease:
+            lease.wait()
+    torch.cuda.synchronize()
+    cache.resident_expert_ids()
+    lease = cache._prefetch_nonblocking(ExpertKey(0, 4))
+    assert lease is not None
+    with lease:
+        assert lease.slot_id == 0
+        actual = lease.wait().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(actual.cpu(), cache._sources[ExpertKey(0, 4)])
+    _close(loaded)
+
+
+def test_speculation_never_queues_a_busy_slot_wait(device):
+    loaded, _, _ = _case(slots=1, layers=1)
+    cache = loaded.expert_caches[0]
+    use = torch.cuda.Stream()
+    with cache.acquire(ExpertKey(0, 0)) as lease:
+        with torch.cuda.stream(use):
+            torch.cuda._sleep(50_000_000)
+            preserved = lease.wait(use).clone()
+    before = cache.stats().h2d_submissions
+    assert cache._prefetch_nonblocking(ExpertKey(0, 1)) is None
+    assert cache.stats().h2d_submissions == before
+    with cache._prefetch(ExpertKey(0, 1)) as lease:
+        lease.wait()
+    torch.cuda.synchronize()
+    assert torch.equal(preserved.cpu(), cache._sources[ExpertKey(0, 0)])
+    _close(loaded)
+
+
+def test_cross_layer_submission_is_observable(device):
+    for depth in (0, 1):
+        loaded, _, inputs = _case(slots=6)
+        for e in range(5):
+            with loaded.expert_caches[0].acquire(ExpertKey(0, e)) as lease:
+                lease.wait()
+        torch.cuda.synchronize()
+        with loaded.prefetch_experts({0: list(range(5)), 1: list(range(5))},
+                                     lookahead_layers=depth, trace=True) as sched:
+            loaded.model(*inputs)
+        events = sched.events()
+        attention = next(e["sequence"] for e in events if e["action"] == "attention" and e["layer_id"] == 1)
+        router = next(e["sequence"] for e in events if e["action"] == "router" and e["layer_id"] == 1)
+        copies = [e for e in events if e["action"] == "copy" and e["layer_id"] == 1]
+        assert any(e["sequence"] < router for e in copies)
+        assert any(e["sequence"] < attention for e in copies) == bool(depth)
+        _close(loaded)
+
+
+def test_predicted_residents_survive_earlier_missing_predictions(device):
+    for depth in (0, 1):
+        for limit in (None, 1):
+            loaded, observer, original = _case(slots=3)
+            inputs = (original[0], torch.tensor([[0, 2]] * 4, device="cuda:0"), original[2][:, :2])
+            expected = loaded.model(*inputs)
+            loaded.cold_reset_expert_caches()
+            for lid, cache in enumerate(loaded.expert_caches):
+                for e in (2, 1, 3):
+                    with cache.acquire(ExpertKey(lid, e)) as lease:
+                        lease.wait()
+            torch.cuda.synchronize()
+            before = [c.stats().h2d_submissions for c in loaded.expert_caches]
+            start = len(observer.events())
+            streams = tuple(c.copy_stream for c in loaded.expert_caches)
+            with loaded.prefetch_experts({0: (0, 2), 1: (0, 2)}, lookahead_layers=depth,
+                                         max_prefetch_per_layer=limit):
+                actual = loaded.model(*inputs)
+            assert torch.equal(actual, expected)
+            _assert_restored(loaded, streams)
+            for lid, cache in enumerate(loaded.expert_caches):
+                assert cache.stats().h2d_submissions - before[lid] == 1
+            assert not any(e.kind is RuntimeEventKind.EVICT and e.victim_expert_id.expert_id == 2
+                           for e in observer.events()[start:])
+            _close(loaded)
+
+
+def test_entry_failure_and_injected_errors_restore_everything(device):
+    loaded, _, inputs = _case()
+    streams = tuple(c.copy_stream for c in loaded.expert_caches)
+    cache = loaded.expert_caches[0]
+    with cache.acquire(ExpertKey(0, 0)) as lease:
+        lease.wait()
+    torch.cuda.synchronize()
+    original = cache._prefetch_nonblocking
+
+    def fail(key, **kwargs):
+        if key.expert_id == 1:
+            raise RuntimeError("injected entry failure")
+        return original(key, **kwargs)
+
+    with patch.object(cache, "_prefetch_nonblocking", fail):
+        with pytest.raises(RuntimeError, match="injected entry failure"):
+            with loaded.prefetch_experts({0: (0, 1)}):
+                pass
+    _assert_restored(loaded, streams)
+    loaded.model(*inputs)
+    for name in ("_dispatch", "_expert_forward"):
+        with pytest.raises(RuntimeError, match="injected"):
+            with loaded.prefetch_experts({0: (0, 1), 1: (0, 1)}) as sched:
+                with patch.object(implementation, name, side_effect=RuntimeError("injected")):
+                    loaded.model(*inputs)
+        assert not sched.stats()["complete"]
+        _assert_restored(loaded, streams)
+        loaded.model(*inputs)
+    _close(loaded)
+
+
+def test_current_demand_precedes_future_predictions(device):
+    loaded, _, inputs = _case(slots=6)
+    with loaded.prefetch_experts({1: (0, 1, 2, 3, 4)}, trace=True) as sched:
+        loaded.model(*inputs)
+    events = sched.events()
+    router = next(e["sequence"] for e in events if e["action"] == "router" and e["layer_id"] == 0)
+    current = [e["sequence"] for e in events if e["action"] == "copy" and e["layer_id"] == 0]
+    future = [e["sequence"] for e in events if e["action"] == "copy" and e["layer_id"] == 1
+              and e["sequence"] > router]
+    assert current
+    if future:
+        assert max(current) < min(future)
+    _close(loaded)
+
+
+def test_prior_inflight_prediction_is_joined(device):
+    loaded, observer, inputs = _case(slots=3, layers=1)
+    cache = loaded.expert_caches[0]
+    with torch.cuda.stream(cache.copy_stream):
+        torch.cuda._sleep(50_000_000)
+    cache._prefetch(ExpertKey(0, 0)).release()
+    with loaded.prefetch_experts({0: (0, 1)}, trace=True):
+        loaded.model(*inputs)
+    submits = [e for e in observer.events() if e.kind is RuntimeEventKind.H2D_SUBMIT
+               and e.expert_id == ExpertKey(0, 0)]
+    assert len(submits) == 1
+    _close(loaded)
+
+
+def test_invalid_configuration_and_context_misuse(device):
+    loaded, _, inputs = _case()
+    before = [c.stats() for c in loaded.expert_caches]
+    for predictions, kwargs in (({2: (0,)}, {}), ({0: (6,)}, {}), ({0: (True,)}, {}),
+                                ({0: (0,), 1: (6,)}, {}), ({0: (-1,)}, {}), ({0: (0.,)}, {}),
+                                ({0: ("0",)}, {}), ({}, {"lookahead_layers": -1}),
+                                ({}, {"max_inflight": 0}), ({}, {"max_inflight": True}),
+                                ({}, {"max_prefetch_per_layer": -1})):
+        with pytest.raises(ValueError):
+            loaded.prefetch_experts(predictions, **kwargs)
+        assert [c.stats() for c in loaded.expert_caches] == before
+    with loaded.prefetch_experts({}) as sched:
+        with pytest.raises(RuntimeError, match="context is active"):
+            with loaded.prefetch_experts({}):
+                pass
+        for op in (lambda: loaded.set_expert_h2d_prefetch(False),
+                   lambda: loaded.set_expert_execution_policy("resident_first"), loaded.close):
+            with pytest.raises(RuntimeError, match="predicted prefetch"):
+                op()
+        loaded.model(*inputs)
+    with pytest.raises(RuntimeError, match="reused"):
+        with sched:
+            pass
+    streams = tuple(c.copy_stream for c in loaded.expert_caches)
+    with pytest.raises(RuntimeError, match="complete target forward"):
+        with loaded.prefetch_experts({}):
+            pass
+    with pytest.raises(RuntimeError, match="ordered eager"):
+        with loaded.prefetch_experts({}):
+            loaded.model(*inputs)
+            loaded.model(*inputs)
+    _assert_restored(loaded, streams)
+    _close(loaded)
+
+
+# ------------------------------------------------------------------ loader --
+def _tiny_config(layers=1):
+    from transformers import Qwen3MoeConfig
+    return Qwen3MoeConfig(dtype=torch.bfloat16, vocab_size=64, hidden_size=32, intermediate_size=48,
+                          moe_intermediate_size=16, num_hidden_layers=layers,
+                          num_attention_heads=4, num_key_value_heads=2, num_experts=4,
+                          num_experts_per_tok=2, max_position_embeddings=64, bos_token_id=1,
+                          eos_token_id=2, pad_token_id=0, use_cache=True)
+
+
+def _save_qwen3_style_checkpoint(model, root):
+    """Per-expert key layout of the original Qwen3 checkpoints."""
+    from safetensors.torch import save_file
+    root = Path(root)
+    model.config.save_pretrained(root)
+    out = {}
+    I = model.config.moe_intermediate_size
+    for name, tensor in model.state_dict().items():
+        if name.endswith(".experts.gate_up_proj"):
+            prefix = name[: -len("gate_up_proj")]
+            for e in range(model.config.num_experts):
+                out[f"{prefix}{e}.gate_proj.weight"] = tensor[e, :I].contiguous()
+                out[f"{prefix}{e}.up_proj.weight"] = tensor[e, I:].contiguous()
+        elif name.endswith(".experts.down_proj"):
+            prefix = name[: -len("down_proj")]
+            for e in range(model.config.num_experts):
+                out[f"{prefix}{e}.down_proj.weight"] = tensor[e].contiguous()
+        else:
+            out[name] = tensor.contiguous()
+    shard = "model-00001-of-00001.safetensors"
+    save_file(out, root / shard)
+    (root / "model.safetensors.index.json").write_text(
+        json.dumps({"metadata": {}, "weight_map": {n: shard for n in out}}), encoding="utf-8")
+
+
+def test_loader_matches_hf_eager_and_switches_policies(device):
+    from transformers import Qwen3MoeForCausalLM
+    torch.manual_seed(918)
+    source = Qwen3MoeForCausalLM(_tiny_config(2)).to(torch.bfloat16)
+    source.config._experts_implementation = "eager"
+    ids = torch.tensor([[1, 7, 11, 19]])
+    with torch.inference_mode():
+        hf = source(ids, use_cache=False).logits.float()
+    with tempfile.TemporaryDirectory() as root:
+        _save_qwen3_style_checkpoint(source, root)
+        with load_offloaded_qwen3(root, device=device, slots_per_layer=2, h2d_prefetch=False) as loaded:
+            modules = [layer.mlp.experts for layer in loaded.model.model.layers]
+            assert all(m.h2d_prefetch is False for m in modules)
+            with torch.inference_mode():
+                expected = loaded.model(ids.to(device), use_cache=False).logits
+                for enabled in (True, False):
+                    loaded.cold_reset_expert_caches()
+                    loaded.set_expert_h2d_prefetch(enabled)
+                    assert torch.equal(expected, loaded.model(ids.to(device), use_cache=False).logits)
+                for depth in (0, 1):
+                    loaded.cold_reset_expert_caches()
+                    with loaded.prefetch_experts({}, lookahead_layers=depth) as sched:
+                        actual = loaded.model(ids.to(device), use_cache=False).logits
+                    assert torch.equal(actual, expected) and sched.stats()["complete"]
+            with pytest.raises(ValueError):
+                loaded.set_expert_h2d_prefetch("false")
+            with loaded.expert_caches[-1].acquire(ExpertKey(1, 0)):
+                with pytest.raises(RuntimeError, match="active leases"):
+                    loaded.set_expert_h2d_prefetch(True)
+            torch.testing.assert_close(expected.float().cpu(), hf, rtol=3e-2, atol=3e-2)
+        with pytest.raises(RuntimeError, match="open caches"):
+            loaded.set_expert_h2d_prefetch(True)
