@@ -117,7 +117,11 @@ int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
  * bf16, as written by the reference's packed checkpoint.
  *   max_rows        an upper bound on the rows of any listed expert (any
  *                   value >= 1 is correct; tokens * top_k always is).  It
- *                   picks the MFMA tile count per pass, i.e. only speed.
+ *                   picks the MFMA rows per pass, i.e. only speed.
+ * The MFMA kernels cover the Qwen3-30B-A3B expert shape (hidden 2048,
+ * intermediate 768) with 16-byte aligned buffers; other shapes run fp32
+ * loop kernels with the same rounding points.  The fp32 summation order of
+ * an output depends on the shape and on its expert's row count only.
  *   expert_ids      host int32 [n_experts]: experts computed by this call
  *   expert_weights  host uint64 [n_experts]: device address of each expert's
  *                   packed weights (a cache slot)

@@ -7,32 +7,33 @@
 //
 // At verification sizes an expert sees m <= a few dozen rows, so each weight
 // element is used m times and the GEMMs are bound by streaming the 9 MiB of
-// expert weights from HBM.  Every weight byte is read exactly once.
+// expert weights from HBM.  Every weight byte is read from HBM once.
 //
-// Weight access pattern.  A 16x16x32 MFMA B operand, loaded directly, touches
-// 16 weight rows x 64 B per load instruction; on MI355X that pattern streams
-// HBM at ~4.4 TB/s, while row-contiguous 1 KiB loads stream at ~6.2 TB/s.  So
-// weights are read as blocks of 2 rows x 512 B per instruction (256 k per
-// row), written to a wavefront-private, row-padded LDS tile (16 B of padding
-// per row keeps the transposed reads free of bank conflicts) and read back in
-// MFMA-operand order.  Token rows (the A operand, a few KiB, L2 resident) are
-// loaded straight into registers.
+// Weight stream.  A workgroup owns a slab of 16*NT weight rows (phase 1: the
+// 16 gate + 16 up rows of 16 activation columns; phase 2: 64 rows of D, i.e.
+// 64 output columns) and streams it in blocks of 256 k.  A block is loaded
+// row-contiguously (2 rows x 512 B per wavefront instruction, ~6.2 TB/s on
+// MI355X, where loading MFMA B fragments directly touches 16 rows x 64 B per
+// instruction and streams at ~4.4 TB/s), two blocks ahead into registers,
+// then written to one of two row-padded LDS tiles (16 B of padding per row
+// keeps the fragment reads conflict-free) and read back as MFMA B fragments.
+// Token rows (the A operand, a few KiB, L2 resident) are loaded straight into
+// registers together with the block they multiply.  The block count is a
+// compile-time constant of the expert shape, so the loop is unrolled and
+// every load is unconditional: the compiler's vector-memory wait counts are
+// then exact (they are in-order counters; a conditional load would force a
+// full drain).
 //
-// Phase 1 (gate/up): a workgroup owns 16 activation columns of one expert,
-// i.e. 16 gate rows + 16 up rows of GU.  Its 4 wavefronts split H into
-// quarters; partial tiles are summed in LDS in wavefront order
-// (deterministic), then the SwiGLU epilogue writes bf16 activations.
-// Phase 2 (down): a workgroup owns 64 output columns (4 wavefronts x 16) of
-// one expert over the full I; the epilogue applies the routing weight.
-//
-// Rows per pass: each workgroup picks 1, 2 or 4 sixteen-row MFMA tiles from
-// its own expert's row count (capped by the launch's max_rows), so small
-// experts do not pay for the largest expert of a launch.  Rows past the end
-// of a pass repeat the pass's last row: an MFMA output row depends only on
-// its own A row and rows past the end are never stored, so the loads need
-// no per-lane branches.  The fp32 summation order of every output is fixed
-// by (H, I) alone, so results do not depend on grouping, tile count or
-// launch.
+// Work split of a pass.  The 4 wavefronts cover TM sixteen-row token tiles x
+// KS k-slices (TM * KS = 4), chosen per workgroup from its expert's row
+// count m: m <= 16 -> 1 x 4, m <= 32 -> 2 x 2, larger -> 4 x 1 (and two tiles
+// per wavefront, 128 rows per pass, when the launch has experts above 64
+// rows).  K-slice partial sums are added in LDS in slice order.  So the fp32
+// summation order of an output depends only on (H, I) and the expert's own
+// m, never on the launch, its grouping or max_rows.  Rows past the end of a
+// pass repeat the pass's last row: an MFMA output row depends only on its
+// own A row and such rows are never stored, so loads need no per-lane
+// branches.
 // MFMA: v_mfma_f32_16x16x32_bf16, A = token rows (M), B = weight rows (N).
 #include "sf_common.h"
 
@@ -42,7 +43,7 @@ constexpr int kMaxListExperts = 128;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / SF_WAVE;
 constexpr int kGateCols = 16;          // activation columns per phase-1 workgroup
-constexpr int kDownCols = 16 * kWaves; // output columns per phase-2 workgroup
+constexpr int kDownCols = 64;          // output columns per phase-2 workgroup
 constexpr int kBlockK = 256;           // k per staged weight block
 constexpr int kRowBytes = kBlockK * 2 + 16;  // padded LDS row (bytes)
 
@@ -108,214 +109,315 @@ __device__ __forceinline__ sf_bf16x8 as_bf16x8(uint4 v) {
   return __builtin_bit_cast(sf_bf16x8, v);
 }
 
+// Global-memory 16-byte load.  The explicit global address space keeps the
+// load a global_load (a flat load also counts against the LDS counter, which
+// forces full drains at every LDS wait).
+typedef unsigned int sf_u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
-  return *reinterpret_cast<const uint4*>(p);
+  const sf_u32x4 v = *(const __attribute__((address_space(1))) sf_u32x4*)(p);
+  return __builtin_bit_cast(uint4, v);
 }
 
 __device__ __forceinline__ sf_f32x4 mfma16(uint4 a, uint4 b, sf_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
-// Stage ROWS (even) weight rows x kBlockK k into a wavefront's LDS tile:
-// lane l loads 16 B of row 2i + l/32 at k offset 8*(l%32); row r of the
-// block starts at w_row0 + r * row_stride.
-template <int ROWS>
-__device__ __forceinline__ void stage_block(const uint16_t* w_row0, int64_t row_stride,
-                                            char* tile, int lane) {
-  const int half = lane >> 5;
-  const int col = (lane & 31) * 8;
-  uint4 v[ROWS / 2];
+
+// ------------------------------------------------------ streaming core --
+constexpr int kSteps = kBlockK / 32;  // MFMA k-steps per block
+constexpr int kDepth = 2;             // blocks in flight ahead of the one in use
+
+// A weight slab: rows 16g .. 16g+15 start at group[g] and are `stride`
+// elements apart.
+template <int NT>
+struct Slab {
+  const uint16_t* group[NT];
+  int64_t stride;
+};
+
+// Lane l of wavefront w loads 16 B of slab rows 8i + 2w + l/32 (i < 2*NT) at
+// k 8*(l%32) of block b.
+template <int NT>
+__device__ __forceinline__ void load_w(const Slab<NT>& w, int b, int lane, int wave,
+                                       uint4 (&r)[2 * NT]) {
+  const int col = b * kBlockK + (lane & 31) * 8;
 #pragma unroll
-  for (int i = 0; i < ROWS / 2; ++i)
-    v[i] = ld16(w_row0 + static_cast<int64_t>(2 * i + half) * row_stride + col);
-#pragma unroll
-  for (int i = 0; i < ROWS / 2; ++i)
-    *reinterpret_cast<uint4*>(tile + (2 * i + half) * kRowBytes + col * 2) = v[i];
+  for (int i = 0; i < 2 * NT; ++i) {
+    const int row = 8 * (i & 1) + 2 * wave + (lane >> 5);
+    r[i] = ld16(w.group[i >> 1] + static_cast<int64_t>(row) * w.stride + col);
+  }
 }
 
-// MFMA B fragment of k-step s (32 k) for tile rows [r0, r0 + 16): lane l
-// takes row r0 + l%16, k 8*(l/16) .. +7 of the step.
+template <int NT>
+__device__ __forceinline__ void store_w(char* tile, int lane, int wave, const uint4 (&r)[2 * NT]) {
+  const int colb = (lane & 31) * 16;
+#pragma unroll
+  for (int i = 0; i < 2 * NT; ++i) {
+    const int row = 8 * i + 2 * wave + (lane >> 5);
+    *reinterpret_cast<uint4*>(tile + row * kRowBytes + colb) = r[i];
+  }
+}
+
+// MFMA B fragment of k-step s for tile rows [r0, r0 + 16): lane l takes row
+// r0 + l%16, k 8*(l/16) .. +7 of the step.
 __device__ __forceinline__ uint4 frag_b(const char* tile, int r0, int s, int lane) {
   return *reinterpret_cast<const uint4*>(tile + (r0 + (lane & 15)) * kRowBytes + s * 64 +
                                          (lane >> 4) * 16);
 }
 
-// Sixteen-row tiles needed by an expert of m rows, capped at MTMAX.
-template <int MTMAX>
-__device__ __forceinline__ int tiles_for(int m) {
-  return (min(m, 16 * MTMAX) + 15) / 16;
+// A fragments of the SP k-steps of one block that a wavefront's slice uses.
+template <int MTW, int SP>
+__device__ __forceinline__ void load_x(const uint16_t* const (&xr)[MTW], int b, int s0,
+                                       uint4 (&x)[MTW][SP]) {
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+    for (int s = 0; s < SP; ++s) x[mt][s] = ld16(xr[mt] + b * kBlockK + (s0 + s) * 32);
+}
+
+// MFMAs of one block: B fragments are read in groups ahead of their MFMAs
+// (the scheduling barrier keeps the group's LDS reads together, so their
+// latency is paid once per group).
+template <int NT, int MTW, int SP>
+__device__ __forceinline__ void mfma_block(const char* tile, int s0, const uint4 (&x)[MTW][SP],
+                                           int lane, sf_f32x4 (&acc)[MTW][NT]) {
+  constexpr int kGroup = (NT <= 2 ? 4 : 2) < SP ? (NT <= 2 ? 4 : 2) : SP;
+#pragma unroll
+  for (int g = 0; g < SP; g += kGroup) {
+    uint4 f[kGroup][NT];
+#pragma unroll
+    for (int s = 0; s < kGroup; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) f[s][nt] = frag_b(tile, 16 * nt, s0 + g + s, lane);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < kGroup; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt) acc[mt][nt] = mfma16(x[mt][g + s], f[s][nt], acc[mt][nt]);
+  }
+}
+
+// acc = X . W^T over k-slice `slice` of KS (SP = kSteps/KS k-steps of each of
+// the NB blocks).  active: wave-uniform, false when the wavefront's tiles
+// have no rows (its A loads then hit one cache line, see a_rows).
+template <int NT, int MTW, int KS, int NB>
+__device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* const (&xr)[MTW],
+                                            int slice, bool active, char* smem,
+                                            sf_f32x4 (&acc)[MTW][NT]) {
+  static_assert(NB >= kDepth, "fewer blocks than the prefetch depth");
+  constexpr int SP = kSteps / KS;
+  constexpr int kTile = 16 * NT * kRowBytes;
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+  const int wave = threadIdx.x / SF_WAVE;
+  const int s0 = slice * SP;
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+  uint4 wr[kDepth][2 * NT];
+  uint4 xq[kDepth][MTW][SP];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) {
+    load_w<NT>(w, d, lane, wave, wr[d]);
+    load_x<MTW, SP>(xr, d, s0, xq[d]);
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int d = b % kDepth;
+    char* tile = smem + (b & 1) * kTile;
+    store_w<NT>(tile, lane, wave, wr[d]);
+    uint4 xc[MTW][SP];
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+      for (int s = 0; s < SP; ++s) xc[mt][s] = xq[d][mt][s];
+    if (b + kDepth < NB) {  // resolved at compile time
+      load_w<NT>(w, b + kDepth, lane, wave, wr[d]);
+      load_x<MTW, SP>(xr, b + kDepth, s0, xq[d]);
+    }
+    __syncthreads();  // tile b visible; tile b-1's reads are done
+    if (active) mfma_block<NT, MTW, SP>(tile, s0, xc, lane, acc);
+  }
+  __syncthreads();  // the tiles are free again
+}
+
+// Adds the KS k-slice partial sums of each tile in slice order, in LDS.
+// Returns true for the wavefront that holds the total (slice 0).
+template <int NT, int KS>
+__device__ __forceinline__ bool reduce_slices(sf_f32x4 (&acc)[1][NT], char* smem) {
+  if (KS == 1) return true;
+  constexpr int TM = kWaves / KS;
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+  const int wave = threadIdx.x / SF_WAVE;
+  const int t = wave % TM;
+  const int q = wave / TM;
+  float* part = reinterpret_cast<float*>(smem);  // [KS][TM][NT][4][64], lane-major
+  if (q > 0) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[(((q * TM + t) * NT + nt) * 4 + i) * 64 + lane] = acc[0][nt][i];
+  }
+  __syncthreads();
+  if (q == 0) {
+#pragma unroll
+    for (int qq = 1; qq < KS; ++qq)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[0][nt][i] += part[(((qq * TM + t) * NT + nt) * 4 + i) * 64 + lane];
+  }
+  __syncthreads();
+  return q == 0;
+}
+
+// Lane row pointers of a wavefront's A tiles (tile mt*TM + wave%TM of the
+// pass, row 16*tile + l%16 clamped to the pass, + the lane's k offset).  An
+// idle wavefront points every lane at the pass's first row.
+template <int MTW, int TM, typename RowPtr>
+__device__ __forceinline__ bool a_rows(RowPtr row_of, int mp, const uint16_t* (&xr)[MTW]) {
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+  const int wave = threadIdx.x / SF_WAVE;
+  const int t0 = wave % TM;
+  const bool active = t0 * 16 < mp;
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt) {
+    if (active)
+      xr[mt] = row_of(min((mt * TM + t0) * 16 + (lane & 15), mp - 1)) + 8 * (lane >> 4);
+    else
+      xr[mt] = row_of(0);
+  }
+  return active;
 }
 
 // ---------------------------------------------------------------- phase 1 --
-template <Resolve R, int MT>
+// Workgroup: 16 activation columns c0.. of one expert = gate rows c0.. and up
+// rows I + c0.. of GU (NT = 2).
+template <Resolve R, int MTW, int KS, int NB>
 __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWork& wk, int tile,
                                             char* smem) {
-  constexpr int kRows = 16 * MT;
-  auto s_part = reinterpret_cast<float(*)[2][kRows][kGateCols]>(smem);
-  auto s_w = reinterpret_cast<char(*)[32 * kRowBytes]>(smem);
+  constexpr int TM = kWaves / KS;
+  constexpr int kPass = 16 * TM * MTW;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int H = a.H;
   const int c0 = tile * kGateCols;
-  const int kq = H / kWaves;
-  const int kbeg = wave * kq;
-  const int lrow = lane & 15;
-  const int kl = 8 * (lane >> 4);
-  char* wt = s_w[wave];
-  // LDS tile rows 0..15: gate rows c0.., rows 16..31: up rows I + c0..
-  const uint16_t* wgate = wk.w + static_cast<int64_t>(c0) * H + kbeg;
-  const uint16_t* wup = wk.w + static_cast<int64_t>(a.I + c0) * H + kbeg;
-  const int blocks = kq / kBlockK;
-
-  for (int p0 = 0; p0 < wk.m; p0 += kRows) {
-    const int mp = min(kRows, wk.m - p0);
-    const uint16_t* xr[MT];
+  Slab<2> w;
+  w.group[0] = wk.w + static_cast<int64_t>(c0) * H;
+  w.group[1] = wk.w + static_cast<int64_t>(a.I + c0) * H;
+  w.stride = H;
+  for (int p0 = 0; p0 < wk.m; p0 += kPass) {
+    const int mp = min(kPass, wk.m - p0);
+    const uint16_t* xr[MTW];
+    const bool active = a_rows<MTW, TM>(
+        [&](int row) { return row_ptr<R>(a, wk.r0 + p0 + row); }, mp, xr);
+    sf_f32x4 acc[MTW][2];
+    stream_gemm<2, MTW, KS, NB>(w, xr, wave / TM, active, smem, acc);
+    bool owner = true;
+    if constexpr (KS > 1) owner = reduce_slices<2, KS>(acc, smem);
+    if (!owner) continue;
+    // D layout: lane holds rows 4*(lane/16)+i, column lane%16.
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      xr[mt] = row_ptr<R>(a, wk.r0 + p0 + min(mt * 16 + lrow, mp - 1)) + kbeg + kl;
-    sf_f32x4 acc[MT][2];
+    for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      acc[mt][0] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-      acc[mt][1] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int b = 0; b < blocks; ++b) {
-      stage_block<16>(wgate + b * kBlockK, H, wt, lane);
-      stage_block<16>(wup + b * kBlockK, H, wt + 16 * kRowBytes, lane);
-#pragma unroll
-      for (int s = 0; s < kBlockK / 32; ++s) {
-        uint4 x[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) x[mt] = ld16(xr[mt] + b * kBlockK + s * 32);
-        const uint4 g = frag_b(wt, 0, s, lane);
-        const uint4 u = frag_b(wt, 16, s, lane);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          acc[mt][0] = mfma16(x[mt], g, acc[mt][0]);
-          acc[mt][1] = mfma16(x[mt], u, acc[mt][1]);
+      for (int i = 0; i < 4; ++i) {
+        const int row = (mt * TM + wave % TM) * 16 + 4 * (lane >> 4) + i;
+        if (row < mp) {
+          const float gb = sf_round_bf16(acc[mt][0][i]);
+          const float ub = sf_round_bf16(acc[mt][1][i]);
+          const float sb = sf_round_bf16(sf_silu(gb));
+          a.act[static_cast<int64_t>(wk.r0 + p0 + row) * a.I + c0 + (lane & 15)] =
+              sf_f32_to_bf16(sb * ub);
         }
       }
     }
-    __syncthreads();  // every wavefront is done with its weight tile
-    // D layout: lane holds rows 4*(lane/16)+i, column lane%16.
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = mt * 16 + 4 * (lane >> 4) + i;
-        s_part[wave][0][row][lrow] = acc[mt][0][i];
-        s_part[wave][1][row][lrow] = acc[mt][1][i];
-      }
-    }
-    __syncthreads();
-    for (int q = threadIdx.x; q < mp * kGateCols; q += kThreads) {
-      const int row = q / kGateCols;
-      const int col = q - row * kGateCols;
-      float g = s_part[0][0][row][col];
-      float up = s_part[0][1][row][col];
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w) {
-        g += s_part[w][0][row][col];
-        up += s_part[w][1][row][col];
-      }
-      const float gb = sf_round_bf16(g);
-      const float ub = sf_round_bf16(up);
-      const float sb = sf_round_bf16(sf_silu(gb));
-      a.act[static_cast<int64_t>(wk.r0 + p0 + row) * a.I + c0 + col] = sf_f32_to_bf16(sb * ub);
-    }
-    __syncthreads();
   }
 }
 
-template <Resolve R, int MTMAX>
+template <Resolve R, int MTW, int NB>
 __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const SwigluArgs a) {
-  // The weight tiles are dead once the K loop ends, so the cross-wavefront
-  // partial sums reuse their LDS.
-  constexpr int kTileBytes = kWaves * 32 * kRowBytes;
-  constexpr int kPartBytes = kWaves * 2 * 16 * MTMAX * kGateCols * 4;
-  __shared__ __attribute__((aligned(16))) char smem[kTileBytes > kPartBytes ? kTileBytes : kPartBytes];
+  __shared__ __attribute__((aligned(16))) char smem[2 * 32 * kRowBytes];
   const int tiles = a.I / kGateCols;
   const int j = blockIdx.x / tiles;
   const int tile = blockIdx.x - j * tiles;
   ExpertWork wk;
   if (!resolve<R>(a, j, wk)) return;
-  const int need = tiles_for<MTMAX>(wk.m);
-  if (MTMAX >= 4 && need > 2)
-    gateup_body<R, 4>(a, wk, tile, smem);
-  else if (MTMAX >= 2 && need > 1)
-    gateup_body<R, 2>(a, wk, tile, smem);
+  if (wk.m <= 16)
+    gateup_body<R, 1, 4, NB>(a, wk, tile, smem);
+  else if (wk.m <= 32)
+    gateup_body<R, 1, 2, NB>(a, wk, tile, smem);
+  else if (MTW >= 2 && wk.m > 64)
+    gateup_body<R, 2, 1, NB>(a, wk, tile, smem);
   else
-    gateup_body<R, 1>(a, wk, tile, smem);
+    gateup_body<R, 1, 1, NB>(a, wk, tile, smem);
 }
 
 // ---------------------------------------------------------------- phase 2 --
-template <Resolve R, int MT>
+// Workgroup: kDownCols output columns n0.. of one expert over the full I.
+template <Resolve R, int MTW, int KS, int NB>
 __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork& wk, int tile,
                                           char* smem) {
-  constexpr int kRows = 16 * MT;
-  auto s_w = reinterpret_cast<char(*)[16 * kRowBytes]>(smem);
+  constexpr int NT = kDownCols / 16;
+  constexpr int TM = kWaves / KS;
+  constexpr int kPass = 16 * TM * MTW;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int I = a.I;
-  const int n0 = tile * kDownCols + wave * 16;
-  const int lrow = lane & 15;
-  const int kl = 8 * (lane >> 4);
-  char* wt = s_w[wave];
+  const int n0 = tile * kDownCols;
+  Slab<NT> w;
   const uint16_t* wd = wk.w + 2 * static_cast<int64_t>(a.I) * a.H + static_cast<int64_t>(n0) * I;
-  const int blocks = I / kBlockK;
-
-  for (int p0 = 0; p0 < wk.m; p0 += kRows) {
-    const int mp = min(kRows, wk.m - p0);
-    const uint16_t* ar[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      ar[mt] = a.act + static_cast<int64_t>(wk.r0 + p0 + min(mt * 16 + lrow, mp - 1)) * I + kl;
-    sf_f32x4 acc[MT];
+  for (int g = 0; g < NT; ++g) w.group[g] = wd + static_cast<int64_t>(16 * g) * I;
+  w.stride = I;
+  for (int p0 = 0; p0 < wk.m; p0 += kPass) {
+    const int mp = min(kPass, wk.m - p0);
+    const uint16_t* ar[MTW];
+    const bool active = a_rows<MTW, TM>(
+        [&](int row) { return a.act + static_cast<int64_t>(wk.r0 + p0 + row) * I; }, mp, ar);
+    sf_f32x4 acc[MTW][NT];
+    stream_gemm<NT, MTW, KS, NB>(w, ar, wave / TM, active, smem, acc);
+    bool owner = true;
+    if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
+    if (!owner) continue;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int b = 0; b < blocks; ++b) {
-      stage_block<16>(wd + b * kBlockK, I, wt, lane);
-#pragma unroll
-      for (int s = 0; s < kBlockK / 32; ++s) {
-        uint4 x[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) x[mt] = ld16(ar[mt] + b * kBlockK + s * 32);
-        const uint4 d = frag_b(wt, 0, s, lane);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16(x[mt], d, acc[mt]);
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = mt * 16 + 4 * (lane >> 4) + i;
+        const int row = (mt * TM + wave % TM) * 16 + 4 * (lane >> 4) + i;
         if (row < mp) {
           const int r = wk.r0 + p0 + row;
-          float y = sf_round_bf16(acc[mt][i]);
-          if (a.route_w) y = y * sf_bf16_to_f32(a.route_w[a.perm_pos[r]]);
-          a.out[static_cast<int64_t>(r) * a.H + n0 + lrow] = sf_f32_to_bf16(y);
+          const float rw = a.route_w ? sf_bf16_to_f32(a.route_w[a.perm_pos[r]]) : 1.f;
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            float y = sf_round_bf16(acc[mt][nt][i]);
+            if (a.route_w) y = y * rw;
+            a.out[static_cast<int64_t>(r) * a.H + n0 + 16 * nt + (lane & 15)] = sf_f32_to_bf16(y);
+          }
         }
       }
     }
   }
 }
 
-template <Resolve R, int MTMAX>
+template <Resolve R, int MTW, int NB>
 __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const SwigluArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kWaves * 16 * kRowBytes];
+  __shared__ __attribute__((aligned(16))) char smem[2 * kDownCols * kRowBytes];
   const int tiles = a.H / kDownCols;
   const int j = blockIdx.x / tiles;
   const int tile = blockIdx.x - j * tiles;
   ExpertWork wk;
   if (!resolve<R>(a, j, wk)) return;
-  const int need = tiles_for<MTMAX>(wk.m);
-  if (MTMAX >= 4 && need > 2)
-    down_body<R, 4>(a, wk, tile, smem);
-  else if (MTMAX >= 2 && need > 1)
-    down_body<R, 2>(a, wk, tile, smem);
+  if (wk.m <= 16)
+    down_body<R, 1, 4, NB>(a, wk, tile, smem);
+  else if (wk.m <= 32)
+    down_body<R, 1, 2, NB>(a, wk, tile, smem);
+  else if (MTW >= 2 && wk.m > 64)
+    down_body<R, 2, 1, NB>(a, wk, tile, smem);
   else
-    down_body<R, 1>(a, wk, tile, smem);
+    down_body<R, 1, 1, NB>(a, wk, tile, smem);
 }
 
 // ------------------------------------------------ generic (any shape) path --
@@ -368,18 +470,21 @@ __global__ __launch_bounds__(kThreads) void down_generic_kernel(const SwigluArgs
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Compiled (H, I) block counts of the MFMA path: Qwen3-30B-A3B experts
+// (H = 2048, I = 768).  Other shapes take the generic kernels.
+constexpr int kNbGateup = 8;
+constexpr int kNbDown = 3;
+
 bool mfma_shape_ok(int H, int I) {
-  // phase 1: each wavefront's K range (H/4) is whole staged blocks; phase 2:
-  // I is whole staged blocks and H whole 64-column workgroups.
-  return H % (kWaves * kBlockK) == 0 && H % kDownCols == 0 && I % kGateCols == 0 &&
-         I % kBlockK == 0;
+  return H == kNbGateup * kBlockK && I == kNbDown * kBlockK;
 }
 
 template <Resolve R, int MTMAX>
 int launch_mfma(const SwigluArgs& a, long long g1, long long g2, hipStream_t s) {
-  gateup_mfma_kernel<R, MTMAX><<<dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, s>>>(a);
+  gateup_mfma_kernel<R, MTMAX, kNbGateup>
+      <<<dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
-  down_mfma_kernel<R, MTMAX><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
+  down_mfma_kernel<R, MTMAX, kNbDown><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
   return SF_OK;
 }
@@ -393,9 +498,8 @@ int launch(const SwigluArgs& a, int groups, bool mfma, int max_rows, hipStream_t
     const long long g1 = static_cast<long long>(groups) * (a.I / kGateCols);
     const long long g2 = static_cast<long long>(groups) * (a.H / kDownCols);
     if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
-    if (max_rows <= 16) return launch_mfma<R, 1>(a, g1, g2, s);
-    if (max_rows <= 32) return launch_mfma<R, 2>(a, g1, g2, s);
-    return launch_mfma<R, 4>(a, g1, g2, s);
+    if (max_rows <= 16 * kWaves) return launch_mfma<R, 1>(a, g1, g2, s);
+    return launch_mfma<R, 2>(a, g1, g2, s);
   }
   gateup_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
