@@ -105,6 +105,27 @@ def _union_length(spans) -> float:
     return total
 
 
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "k3_traffic_qwen3_layer_t64_slots24.md")
+
+
+def _traffic_ratio() -> tuple[float | None, str | None]:
+    """(FETCH + WRITE bytes) / expert-weight bytes of the in-step K3
+    dispatches, from the committed counter summary of this workload; the
+    per-launch traffic is this ratio times the launch's weight bytes."""
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            for line in fh:
+                if line.startswith("traffic_ratio_in_step:"):
+                    return float(line.split(":", 1)[1]), (
+                        "profiles/k3_traffic_qwen3_layer_t64_slots24.md: scaled FETCH_SIZE + "
+                        "WRITE_SIZE over expert-weight bytes of the in-step K3 dispatches, "
+                        "times this run's weight bytes per launch")
+    except OSError:
+        pass
+    return None, None
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -220,6 +241,16 @@ def main() -> int:
         t_h2d = _union_length(spans_copy) * 1e-3
         overlap = max(0.0, min(1.0, (t_h2d + t_gemm - t_union) / min(t_h2d, t_gemm)))
 
+    # A plain elementwise kernel of known size (256 MiB read + 256 MiB
+    # written).  Under rocprofv3 --pmc it calibrates FETCH_SIZE / WRITE_SIZE
+    # and separates the in-step K3 dispatches from the all-resident ones
+    # (specfit_amd/pmc.py).
+    cal_src = torch.ones((256 << 20) // 4, dtype=torch.float32, device=dev)
+    cal_dst = torch.empty_like(cal_src)
+    torch.neg(cal_src, out=cal_dst)
+    torch.cuda.synchronize()
+    del cal_src, cal_dst
+
     # Host-link peak: best of 10 x 1 GiB pinned -> device copies.
     flat = layer.experts.view(-1)
     gib = 1 << 30
@@ -270,6 +301,8 @@ def main() -> int:
 
     value = args.steps * T / wall
     k3_achieved = k3_alg / k3_time / 1e9 if k3_time else 0.0
+    ratio, ratio_src = _traffic_ratio()
+    k3_weight_per_launch = sum(n for n, *_ in k3) * expert_bytes / max(len(k3), 1)
     line = {
         "metric": METRIC,
         "value": value,
@@ -292,7 +325,9 @@ def main() -> int:
                    "execution_policy": "resident_first", "h2d_prefetch": True},
         "record": args.record,
         "roofline": {"bound": "hbm", "achieved": k3_achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": k3_achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": k3_achieved / HBM_PEAK_GBS,
+                     "traffic": ratio * k3_weight_per_launch if ratio and k3 else None,
+                     "traffic_source": ratio_src,
                      "kernel": "K3 grouped SwiGLU (gateup_mfma + down_mfma dispatches)",
                      "launches": len(k3), "avg_launch_us": k3_time / max(len(k3), 1) * 1e6,
                      "alg_bytes_per_launch": k3_alg / max(len(k3), 1)},

@@ -18,32 +18,82 @@ from . import _native
 _BF16 = torch.bfloat16
 
 
+_HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # hip_runtime_api.h
+_hip_runtime = None
+
+
+def _hip():
+    global _hip_runtime
+    if _hip_runtime is None:
+        lib = ctypes.CDLL("libamdhip64.so")
+        lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                            ctypes.c_void_p]
+        lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        _hip_runtime = lib
+    return _hip_runtime
+
+
+class TimingEvent:
+    """A HIP timing event recorded without the system-scope fence that
+    ordinary events perform (hipEventDisableSystemFence): no cache
+    writeback/invalidate between the timed kernels, so bracketing every
+    launch does not slow the launches it times.  Same interface as the
+    parts of torch.cuda.Event used here."""
+
+    def __init__(self) -> None:
+        self._ev = ctypes.c_void_p()
+        rc = _hip().hipEventCreateWithFlags(ctypes.byref(self._ev), _HIP_EVENT_DISABLE_SYSTEM_FENCE)
+        if rc:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+
+    def record(self, stream: torch.cuda.Stream) -> None:
+        rc = _hip().hipEventRecord(self._ev, ctypes.c_void_p(int(stream.cuda_stream)))
+        if rc:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end: "TimingEvent") -> float:
+        """Milliseconds from this event to ``end`` (both must have completed)."""
+        ms = ctypes.c_float()
+        rc = _hip().hipEventElapsedTime(ctypes.byref(ms), self._ev, end._ev)
+        if rc:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return float(ms.value)
+
+    def __del__(self) -> None:
+        if self._ev and _hip_runtime is not None:
+            _hip_runtime.hipEventDestroy(self._ev)
+            self._ev = ctypes.c_void_p()
+
+
 class LaunchRecorder:
     """Collects HIP timing events around K3 launches and H2D copies, each on
-    the stream the work runs on (enabled by ``record_launches``)."""
+    the stream the work runs on (enabled by ``record_launches``).  Events
+    are TimingEvents; read them after the device has finished the work."""
 
     def __init__(self, *, copies: bool = True) -> None:
-        self.k3: list[tuple[int, int, str, torch.cuda.Event, torch.cuda.Event]] = []
+        self.k3: list[tuple[int, int, str, TimingEvent, TimingEvent]] = []
         # Copies are timed per window (first copy start .. last copy end of a
         # window, per stream), not per copy: ``close_copy_window`` ends one.
         self.copies = copies
         self.h2d_bytes = 0
         self.h2d_count = 0
-        self.windows: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
-        self._open: dict[int, tuple[torch.cuda.Stream, torch.cuda.Event]] = {}
+        self.windows: list[tuple[TimingEvent, TimingEvent]] = []
+        self._open: dict[int, tuple[torch.cuda.Stream, TimingEvent]] = {}
 
     def _copy_started(self, stream: torch.cuda.Stream, nbytes: int) -> None:
         self.h2d_bytes += nbytes
         self.h2d_count += 1
         key = int(stream.cuda_stream)
         if self.copies and key not in self._open:
-            start = torch.cuda.Event(enable_timing=True)
+            start = TimingEvent()
             start.record(stream)
             self._open[key] = (stream, start)
 
     def close_copy_window(self) -> None:
         for stream, start in self._open.values():
-            end = torch.cuda.Event(enable_timing=True)
+            end = TimingEvent()
             end.record(stream)
             self.windows.append((start, end))
         self._open.clear()
@@ -72,8 +122,8 @@ class LaunchRecorder:
 
     @staticmethod
     def _events(stream):
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
+        start = TimingEvent()
+        end = TimingEvent()
         start.record(stream)
         return start, end
 
