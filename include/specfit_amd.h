@@ -29,6 +29,12 @@
  *                        (index_add_ in canonical or arrival order)
  *   sf_copy_h2d          src/specfit/runtime/gpu_expert_cache.py:556-561
  *                        (slot.tensor.copy_(pinned_source, non_blocking=True))
+ *   sf_tree_attention    the attention of the verification forward:
+ *                        eagle3_tree.py:1202-1240 runs the target with
+ *                        Eagle3DraftTree.verification_attention_mask
+ *                        (eagle3_types.py:450-473); each Qwen3 attention layer
+ *                        then calls transformers sdpa_attention_forward
+ *                        (integrations/sdpa_attention.py) with that mask
  */
 #ifndef SPECFIT_AMD_H
 #define SPECFIT_AMD_H
@@ -40,7 +46,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 2
+#define SF_ABI_VERSION 3
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -189,6 +195,32 @@ int sf_combine(const void *rows, const int64_t *topk_index,
  */
 int sf_copy_h2d(void *device_dst, const void *host_src, size_t bytes,
                 sf_stream_t stream);
+
+/*
+ * K5: grouped-query attention of the verification forward over the cached
+ * prefix plus the draft tree.  For query token qi and query head
+ * qh = h * G + j (G = q_heads / kv_heads, h the key/value head):
+ *   out[qi, qh, :] = sum_s p_s * v[h, s, :],
+ *   p = softmax over admitted keys s of scale * (q[qi, qh, :] . k[h, s, :])
+ * computed in fp32 and rounded to bf16 once.  Key s is admitted when
+ * mask[qi * mask_stride_query + s] != 0; with mask == NULL, when
+ * s <= keys - queries + qi (causal, aligned to the end of the keys).  A
+ * query with no admitted key gets zeros.
+ *   q     bf16, element (qi, qh, d) at qi*q_stride_token + qh*q_stride_head + d
+ *   k, v  bf16, element (h, s, d) at h*stride_head + s*stride_token + d
+ *         (k: 16-byte aligned rows)
+ *   mask  uint8/bool [queries, >= keys] with row stride mask_stride_query
+ *   out   bf16 [queries, q_heads, head_dim], contiguous
+ * head_dim % 8 == 0, head_dim <= 256, G in {1, 2, 4, 8, 16}.
+ */
+int sf_tree_attention(const void *q, int64_t q_stride_token,
+                      int64_t q_stride_head, const void *k,
+                      int64_t k_stride_head, int64_t k_stride_token,
+                      const void *v, int64_t v_stride_head,
+                      int64_t v_stride_token, const uint8_t *mask,
+                      int64_t mask_stride_query, int queries, int keys,
+                      int q_heads, int kv_heads, int head_dim, float scale,
+                      void *out, sf_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -18,7 +18,8 @@ LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libspecfit_amd.so")
 OFFLOAD_ARCH = "gfx950"
 
-SOURCES = ("abi.hip", "router.hip", "dispatch.hip", "swiglu.hip", "combine.hip")
+SOURCES = ("abi.hip", "router.hip", "dispatch.hip", "swiglu.hip", "combine.hip",
+           "attention.hip")
 
 HIPCC_FLAGS = (
     f"--offload-arch={OFFLOAD_ARCH}",

@@ -415,3 +415,49 @@ def copy_h2d(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) ->
         _recorder._copy_started(stream, nbytes)
     rc = _native.lib().sf_copy_h2d(_ptr(dst), _ptr(src), nbytes, int(stream.cuda_stream))
     _native.check(rc, "sf_copy_h2d")
+
+
+# ------------------------------------------------------------------ K5 ----
+def tree_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                   mask: torch.Tensor | None, scale: float, *,
+                   stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Grouped-query attention of the verification forward (K5).
+
+    query [B, Hq, Q, D], key/value [B, Hkv, S, D] bf16 (any strides with a
+    unit last stride), mask [B, 1 or Hq, Q, S] bool (True = attend; the first
+    head's mask is used) or None for causal attention aligned to the end of
+    the keys.  Returns [B, Q, Hq, D] bf16, the layout HF attention functions
+    return."""
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        _require_cuda(name, t, _BF16)
+        if t.dim() != 4 or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be 4-D with a unit last stride")
+    B, Hq, Q, D = query.shape
+    Bk, Hkv, S, Dk = key.shape
+    if key.shape != value.shape or Bk != B or Dk != D:
+        raise ValueError("key/value shapes do not match the query")
+    if Hkv < 1 or Hq % Hkv:
+        raise ValueError("query heads must be a multiple of key/value heads")
+    if mask is not None:
+        if mask.dtype != torch.bool:
+            raise TypeError("tree attention takes a bool mask (True = attend)")
+        if mask.device != query.device or mask.dim() != 4 or mask.shape[0] not in (1, B) \
+                or tuple(mask.shape[2:]) != (Q, S) or mask.stride(-1) != 1:
+            raise ValueError(f"mask must be bool [B, 1, {Q}, {S}] with a unit last stride")
+    out = torch.empty((B, Q, Hq, D), dtype=_BF16, device=query.device)
+    if B == 0 or Q == 0:
+        return out
+    if S == 0:
+        return out.zero_()
+    lib = _native.lib()
+    handle = _stream_handle(stream, query.device)
+    for b in range(B):
+        q, k, v = query[b], key[b], value[b]
+        m = None if mask is None else mask[b if mask.shape[0] == B else 0, 0]
+        rc = lib.sf_tree_attention(
+            q.data_ptr(), q.stride(1), q.stride(0), k.data_ptr(), k.stride(0), k.stride(1),
+            v.data_ptr(), v.stride(0), v.stride(1), None if m is None else m.data_ptr(),
+            0 if m is None else m.stride(0), Q, S, Hq, Hkv, D, float(scale), out[b].data_ptr(),
+            handle)
+        _native.check(rc, "sf_tree_attention")
+    return out

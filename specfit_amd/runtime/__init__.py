@@ -14,6 +14,9 @@ from .qwen3_offloaded_model import (LoadedOffloadedQwen3, Qwen3LoadTimings, buil
 from .qwen3_router import Qwen3MoeTopKRouterHip
 from .state import ExpertKey
 from .trace import RuntimeEventKind
+from .tree_attention import TREE_ATTENTION, register_tree_attention, tree_attention_forward
+from .tree_verify import (Eagle3DraftTree, TreeVerification, compact_tree_cache, synthetic_tree,
+                          verify_draft_tree)
 
 __all__ = [
     "CacheSlotSnapshot", "CacheTransition", "CacheTransitionCounters",
@@ -24,4 +27,6 @@ __all__ = [
     "load_offloaded_qwen3",
     "RecordingCacheTransitionObserver", "ReductionMode", "RuntimeEventKind",
     "aggregate_cache_transition_counters",
+    "Eagle3DraftTree", "TREE_ATTENTION", "TreeVerification", "compact_tree_cache",
+    "register_tree_attention", "synthetic_tree", "tree_attention_forward", "verify_draft_tree",
 ]

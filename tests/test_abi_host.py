@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_error_strings():
-    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 2
+    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 3
     assert _native.error_string(0) == "success"
     assert _native.error_string(1) == "invalid argument"
     assert _native.error_string(12345) != ""
@@ -58,6 +58,20 @@ def test_host_side_validation_needs_no_device():
     assert lib.sf_grouped_swiglu(null, null, null, null, 4, 8, 2048, 768, -1, 1, null, null, null,
                                  null, null) == 1
     assert lib.sf_expert_swiglu(null, 4, 10, 2048, 768, null, null, null, null) == 1
+    # tree attention: bad counts, heads not a multiple, head dim, misaligned keys
+    fake = 4096  # never dereferenced: every case below fails before a launch
+    args = dict(qs=(4096, 128), ks=(1 << 20, 128), mask=(None, 0))
+
+    def attn(q_heads, kv_heads, head_dim, queries=4, keys=8, k=fake):
+        return lib.sf_tree_attention(fake, *args["qs"], k, *args["ks"], fake, *args["ks"],
+                                     *args["mask"], queries, keys, q_heads, kv_heads, head_dim,
+                                     0.1, fake, null)
+    assert attn(32, 4, 128, queries=0) == 1
+    assert attn(32, 5, 128) == 2
+    assert attn(32, 4, 12) == 2
+    assert attn(32, 4, 512) == 2
+    assert attn(96, 4, 128) == 2          # 24 query heads per key/value head
+    assert attn(32, 4, 128, k=fake + 8) == 3
     assert lib.sf_copy_h2d(null, null, 0, null) == 0
     assert lib.sf_copy_h2d(null, null, 16, null) == 1
 
