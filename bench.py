@@ -42,6 +42,19 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU-baseline sample (0 disables it)")
     p.add_argument("--resident-reps", type=int, default=50)
+    p.add_argument("--workload", choices=("layer", "resident16", "sweep", "verify48", "cold48"),
+                   default="layer",
+                   help="layer: one MoE layer, 64 tree tokens, 24-slot cache, Zipf routing (the "
+                        "headline); resident16: 16 tokens, all 128 experts resident, uniform "
+                        "routing; sweep: 1/8/32/64/128 tokens with a 12-slot cache; verify48: "
+                        "the 48-layer verification forward of a 60-node depth-6 tree over a "
+                        "1024-token context with 12-slot caches; cold48: the same forward with "
+                        "128 tree tokens and every cache emptied before each forward")
+    p.add_argument("--layers", type=int, default=48)
+    p.add_argument("--context", type=int, default=1024)
+    p.add_argument("--tree-nodes", type=int, default=60)
+    p.add_argument("--tree-depth", type=int, default=6)
+    p.add_argument("--verify-slots", type=int, default=12)
     p.add_argument("--record", choices=("full", "k3", "none"), default="full",
                    help="timing events in the timed region: K3 launches + one copy window "
                         "per step (full), K3 only, or none")
@@ -137,6 +150,198 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def main_verify(args) -> int:
+    """The 48-layer verification forward: per step, one target forward of
+    [seed, 60 draft nodes] with the tree mask against a 1024-token context
+    (then the context is cropped back), every MoE block offloaded with a
+    12-slot cache and every attention layer on the HIP tree kernel."""
+    import torch
+
+    from specfit_amd import ops
+    from specfit_amd.runtime import synthetic_tree, verify_draft_tree
+    from specfit_amd.workloads import make_kv_context, make_layer, make_verify_model
+
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    experts = make_layer(seed=0, pin_memory=True)
+    loaded = make_verify_model(device=dev, layers=args.layers, slots_per_layer=args.verify_slots,
+                               experts=experts)
+    target = loaded.model
+    config = target.config
+    cache = make_kv_context(config, args.context, device=dev, seed=1)
+    torch.cuda.synchronize()
+    log(f"{args.layers}-layer target built in {time.perf_counter() - t0:.1f}s")
+    n = args.warmup + args.steps
+    trees = [synthetic_tree(args.tree_nodes, args.tree_depth, seed=100 + i,
+                            vocab=config.vocab_size) for i in range(n)]
+    g = torch.Generator().manual_seed(5)
+    seeds = [torch.randint(config.vocab_size, (1, 1), generator=g).to(dev) for _ in range(n)]
+
+    cold = args.workload == "cold48"
+
+    def step(i):
+        res = verify_draft_tree(target, trees[i], seeds[i], cache, commit=False)
+        cache.crop(args.context)
+        return res
+
+    with torch.inference_mode():
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        log("warm-up done")
+        misses = hits = 0
+        with ops.record_launches(copies=True) as rec:
+            wall = 0.0
+            accepted = 0
+            for i in range(args.warmup, n):
+                if cold:  # empty caches (this also clears their counters); not timed
+                    loaded.cold_reset_expert_caches()
+                before = [c.stats() for c in loaded.expert_caches]
+                torch.cuda.synchronize()
+                start = time.perf_counter()
+                accepted += len(step(i).accepted_node_ids)
+                rec.close_copy_window()
+                torch.cuda.synchronize()
+                wall += time.perf_counter() - start
+                after = [c.stats() for c in loaded.expert_caches]
+                misses += sum(a.h2d_submissions - b.h2d_submissions for a, b in zip(after, before))
+                hits += sum(a.resident_hits - b.resident_hits for a, b in zip(after, before))
+                log(f"step {i - args.warmup + 1}/{args.steps}")
+    expert_bytes = experts.expert_bytes
+    H = config.hidden_size
+    k3 = [(nx, rows, tag, s_.elapsed_time(e_) * 1e-3) for nx, rows, tag, s_, e_ in rec.k3]
+    k3_time = sum(x[3] for x in k3)
+    k3_alg = sum(nx * expert_bytes + rows * H * 4 for nx, rows, _, _ in k3)
+    h2d_time = rec.copy_busy_seconds() if rec.windows else 0.0
+    q = 1 + args.tree_nodes
+    value = args.steps * q / wall
+    k3_achieved = k3_alg / k3_time / 1e9 if k3_time else 0.0
+    line = {
+        "metric": "verified tree tokens/s, 48-layer verification forward (1 GPU); achieved HBM "
+                  "GB/s + H2D GB/s",
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init N(0,0.02) bf16 weights (one layer's 128 experts shared by "
+                "every layer's cache), random N(0,1) 1024-token KV context, seeded random trees",
+        "config": {"workload": (f"qwen3-30b-a3b verification forward, {args.layers} layers, "
+                                f"{args.tree_nodes}-node depth-{args.tree_depth} tree over a "
+                                f"{args.context}-token context, {args.verify_slots}-slot LRU expert "
+                                f"cache per layer" + (", caches emptied before every forward"
+                                                      if cold else "")),
+                   "layers": args.layers, "context": args.context, "tree_nodes": args.tree_nodes,
+                   "tree_depth": args.tree_depth, "cache_slots": args.verify_slots,
+                   "attention": "HIP tree attention (K5)",
+                   "execution_policy": "resident_first", "h2d_prefetch": True},
+        "per_layer_tokens_per_s": value * args.layers,
+        "roofline": {"bound": "hbm", "achieved": k3_achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": k3_achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "K3 grouped SwiGLU (gateup_mfma + down_mfma dispatches)",
+                     "launches": len(k3), "avg_launch_us": k3_time / max(len(k3), 1) * 1e6},
+        "cpu_baseline": None,
+        "h2d": {"achieved_gbs": misses * expert_bytes / h2d_time / 1e9 if h2d_time else None,
+                "transfers": misses, "busy_ms": h2d_time * 1e3,
+                "link_busy_frac": h2d_time / wall if h2d_time else None},
+        "cache": {"misses_per_layer": misses / (args.steps * args.layers),
+                  "hits_per_layer": hits / (args.steps * args.layers)},
+        "accepted_per_step": accepted / args.steps,
+    }
+    print(json.dumps(line), flush=True)
+    loaded.close()
+    return 0
+
+
+def main_sweep(args) -> int:
+    """Tree-size sweep: 1, 8, 32, 64 and 128 tokens through one Zipf-routed
+    MoE layer with a 12-slot cache (32 pre-warm cycles per point)."""
+    import torch
+
+    from specfit_amd import ops
+    from specfit_amd.runtime import (ExpertKey, GpuExpertCache, Qwen3MoeTopKRouterHip,
+                                     Qwen3OffloadedExperts)
+    from specfit_amd.workloads import make_hidden, make_layer
+
+    dev = torch.device("cuda:0")
+    layer = make_layer(seed=0, zipf_s=1.1, zipf_lambda=1.0, pin_memory=True)
+    H, I, E, K = layer.hidden_size, layer.intermediate_size, layer.num_experts, layer.top_k
+    router = Qwen3MoeTopKRouterHip(num_experts=E, hidden_size=H, top_k=K, norm_topk_prob=True,
+                                   device=dev)
+    with torch.no_grad():
+        router.weight.copy_(layer.router)
+    points = []
+    slots = 12
+    for T in (1, 8, 32, 64, 128):
+        cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(E)},
+                               slot_count=slots, device=dev, adopt_pinned_sources=True)
+        experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H,
+                                        intermediate_size=I, execution_policy="resident_first",
+                                        h2d_prefetch=True)
+        n = args.prewarm + args.warmup + args.steps
+        hidden = [make_hidden(T, H, seed=1 + i, zipf_fold=True).to(dev) for i in range(n)]
+
+        def step(h):
+            _, w, idx = router(h)
+            return experts(h, idx, w), idx
+
+        for i in range(args.prewarm + args.warmup):
+            step(hidden[i])
+        torch.cuda.synchronize()
+        before = cache.stats()
+        ms = []
+        with ops.record_launches(copies=True) as rec:
+            torch.cuda.synchronize()
+            start = time.perf_counter()
+            idxs = []
+            for h in hidden[args.prewarm + args.warmup:]:
+                idxs.append(step(h)[1])
+                rec.close_copy_window()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - start
+        after = cache.stats()
+        for idx in idxs:
+            counts = torch.bincount(idx.reshape(-1).cpu(), minlength=E)
+            ms.extend(int(c) for c in counts if c > 0)
+        k3 = [(nx, rows, s_.elapsed_time(e_) * 1e-3) for nx, rows, _, s_, e_ in rec.k3]
+        k3_time = sum(x[2] for x in k3)
+        k3_bytes = sum(nx * layer.expert_bytes + rows * H * 4 for nx, rows, _ in k3)
+        k3_weight = sum(nx * layer.expert_bytes for nx, _, _ in k3)
+        k3_flops = sum(2 * rows * 3 * H * I for _, rows, _ in k3)
+        misses = after.h2d_submissions - before.h2d_submissions
+        h2d_time = rec.copy_busy_seconds() if rec.windows else 0.0
+        points.append({
+            "tokens": T, "tokens_per_s": args.steps * T / wall,
+            "ms_per_step": wall / args.steps * 1e3,
+            "misses_per_step": misses / args.steps,
+            "hits_per_step": (after.resident_hits - before.resident_hits) / args.steps,
+            "distinct_experts_per_step": len(ms) / args.steps,
+            "rows_per_expert": {"mean": sum(ms) / len(ms), "max": max(ms)},
+            "k3_flop_per_weight_byte": k3_flops / k3_weight if k3_weight else None,
+            "k3_gbs": k3_bytes / k3_time / 1e9 if k3_time else None,
+            "k3_frac": k3_bytes / k3_time / 1e9 / HBM_PEAK_GBS if k3_time else None,
+            "h2d_gbs": misses * layer.expert_bytes / h2d_time / 1e9 if h2d_time else None,
+            "h2d_link_busy_frac": h2d_time / wall if h2d_time else None,
+        })
+        log(f"T={T}: {points[-1]['tokens_per_s']:.0f} tokens/s, "
+            f"{points[-1]['misses_per_step']:.2f} misses/step")
+        cache.close()
+    line = {"metric": "verified tree tokens/s per MoE layer across tree sizes (1 GPU)",
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": True, "dtype": "bf16", "data": "synthetic (as the layer workload)",
+            "config": {"workload": "qwen3-30b-a3b moe layer, 12-slot LRU cache, zipf 1.1, "
+                                   "prewarm 32 cycles, tokens 1/8/32/64/128",
+                       "cache_slots": slots, "prewarm_cycles": args.prewarm},
+            "points": points}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -144,6 +349,14 @@ def main() -> int:
               "(the verification path runs on a single MI355X; multi-GPU sharding is a "
               "design note, not a built path)", file=sys.stderr)
         return 2
+    if args.workload in ("verify48", "cold48"):
+        if args.workload == "cold48" and args.tree_nodes == 60:
+            args.tree_nodes = 127  # 128 tree tokens
+        return main_verify(args)
+    if args.workload == "sweep":
+        return main_sweep(args)
+    if args.workload == "resident16":
+        args.tokens, args.slots = 16, 128
 
     import torch
 
@@ -157,8 +370,10 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     T, slots = args.tokens, args.slots
+    resident = args.workload == "resident16"
     t0 = time.perf_counter()
-    layer = make_layer(seed=0, zipf_s=1.1, zipf_lambda=1.0, pin_memory=True)
+    layer = make_layer(seed=0, zipf_s=None if resident else 1.1, zipf_lambda=1.0,
+                       pin_memory=True)
     H, I, E, K = layer.hidden_size, layer.intermediate_size, layer.num_experts, layer.top_k
     expert_bytes = layer.expert_bytes
     log(f"layer generated in {time.perf_counter() - t0:.1f}s ({E} experts x {expert_bytes} B pinned)")
@@ -174,13 +389,18 @@ def main() -> int:
                                     execution_policy="resident_first", h2d_prefetch=True)
 
     n_inputs = args.prewarm + args.warmup + args.steps
-    hidden = [make_hidden(T, H, seed=1 + i, zipf_fold=True).to(dev) for i in range(n_inputs)]
+    hidden = [make_hidden(T, H, seed=(0 if resident else 1) + i, zipf_fold=not resident).to(dev)
+              for i in range(n_inputs)]
     torch.cuda.synchronize()
 
     def step(h):
         _, w, idx = router(h)
         return experts(h, idx, w)
 
+    if resident:  # every expert in its own slot before the first step
+        for e in range(E):
+            with cache.acquire(ExpertKey(0, e)) as lease:
+                lease.wait()
     # Pre-warm the cache with 32 prior cycles, then untimed warm-up steps.
     for i in range(args.prewarm):
         step(hidden[i])
@@ -301,7 +521,7 @@ def main() -> int:
 
     value = args.steps * T / wall
     k3_achieved = k3_alg / k3_time / 1e9 if k3_time else 0.0
-    ratio, ratio_src = _traffic_ratio()
+    ratio, ratio_src = _traffic_ratio() if not resident else (None, None)
     k3_weight_per_launch = sum(n for n, *_ in k3) * expert_bytes / max(len(k3), 1)
     line = {
         "metric": METRIC,
@@ -315,11 +535,13 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) hidden states with Zipf(1.1)-biased routing, "
-                "random-init N(0,0.02) bf16 weights",
-        "config": {"workload": "qwen3-30b-a3b moe layer verify, 64 tree tokens, 24-slot LRU "
-                               "expert cache, 128 experts in pinned host memory, zipf 1.1, "
-                               "prewarm 32 cycles",
+        "data": ("synthetic: seeded N(0,1) hidden states, router and experts random-init "
+                 "N(0,0.02) bf16" + ("" if resident else ", Zipf(1.1)-biased routing")),
+        "config": {"workload": ("qwen3-30b-a3b moe layer verify, 16 tree tokens, all 128 experts "
+                                "resident in HBM, uniform routing" if resident else
+                                f"qwen3-30b-a3b moe layer verify, {T} tree tokens, {slots}-slot "
+                                f"LRU expert cache, 128 experts in pinned host memory, zipf 1.1, "
+                                f"prewarm {args.prewarm} cycles"),
                    "tokens": T, "hidden": H, "experts": E, "top_k": K, "intermediate": I,
                    "cache_slots": slots, "prewarm_cycles": args.prewarm,
                    "execution_policy": "resident_first", "h2d_prefetch": True},

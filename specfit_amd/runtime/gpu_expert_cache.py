@@ -264,7 +264,11 @@ class GpuExpertCache:
                     self._record_transition(kind=RuntimeEventKind.RESIDENT_HIT,
                                             expert_id=expert_id, slot=slot)
                 self._stats.resident_hits += 1
-                return self._new_lease(slot, defer_touch=defer_touch)
+                lease = self._new_lease(slot, defer_touch=defer_touch)
+                # Residency is published only after the ready event completed,
+                # so waiting on it again would be a no-op stream wait.
+                lease._ready_known = True
+                return lease
             slot = self._choose_lru_slot()
             if slot is None:
                 raise NoEvictableSlotError("all GPU expert slots have active leases")
@@ -585,6 +589,27 @@ class GpuExpertCache:
             self._validate_lease(slot, expert_id, generation)
             self._record_use_guards(slot, used_streams)
             slot.active_leases -= 1
+
+    def _unpin_many(self, leases) -> None:
+        """``_unpin`` of leases whose weights one launch read: a single use
+        event per stream, recorded after that launch, guards every slot of
+        the batch (it completes no earlier than per-lease events would)."""
+        with self._lock:
+            events: dict[int, torch.cuda.Event] = {}
+            for lease in leases:
+                if not lease._unpin_pending:
+                    continue
+                lease._unpin_pending = False
+                slot = self._slots[lease.slot_id]
+                self._validate_lease(slot, lease.expert_id, lease.generation)
+                for sid, stream in lease._streams.items():
+                    ev = events.get(sid)
+                    if ev is None:
+                        ev = torch.cuda.Event(blocking=False)
+                        ev.record(stream)
+                        events[sid] = ev
+                    slot.use_events[sid] = ev
+                slot.active_leases -= 1
 
     @staticmethod
     def _record_use_guards(slot: _Slot, used_streams: tuple) -> None:

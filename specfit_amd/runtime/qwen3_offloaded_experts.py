@@ -248,8 +248,7 @@ class Qwen3OffloadedExperts(nn.Module):
                             hidden_size=self.hidden_size,
                             intermediate_size=self.intermediate_size, routes=routes)
         finally:
-            for _, lease, _ in batch:
-                lease._unpin()
+            self.cache._unpin_many([lease for _, lease, _ in batch])
 
     def _run_in_order(self, order: tuple[int, ...], routes: _GroupedRoutes) -> None:
         """Reference lease sequence (acquire, optional one-ahead prefetch,

@@ -86,3 +86,71 @@ def make_hidden(tokens: int, hidden_size: int = 2048, *, seed: int,
 def expected_distinct_uniform(tokens: int, num_experts: int = 128, top_k: int = 8) -> float:
     """E[U] of distinct experts under uniform top-k routing."""
     return num_experts * (1.0 - (1.0 - top_k / num_experts) ** tokens)
+
+
+QWEN3_30B_A3B_MODEL = dict(vocab_size=151936, hidden_size=2048, intermediate_size=6144,
+                           moe_intermediate_size=768, num_hidden_layers=48,
+                           num_attention_heads=32, num_key_value_heads=4, head_dim=128,
+                           num_experts=128, num_experts_per_tok=8, norm_topk_prob=True,
+                           rms_norm_eps=1e-6, max_position_embeddings=40960,
+                           tie_word_embeddings=False, decoder_sparse_step=1, mlp_only_layers=[],
+                           rope_parameters={"rope_type": "default", "rope_theta": 1e6})
+
+
+def make_verify_model(*, device, layers: int = 48, slots_per_layer: int = 12, seed: int = 0,
+                      experts: MoELayerWeights | None = None, std: float = 0.02,
+                      expert_execution_policy: str = "resident_first"):
+    """A Qwen3-30B-A3B-shaped target for the verification forward, random
+    init: every non-expert weight N(0, std) bf16 (norm weights 1), drawn on
+    the device from a seeded generator; the routed experts of every layer
+    are the pinned packed experts of ``experts`` (one MoE layer's worth,
+    shared by all layers so the host holds 1.2 GB instead of 58 GB; every
+    layer still has its own slot cache and copies its own misses).  The
+    attention layers run the HIP tree-attention kernel.  Returns the
+    LoadedOffloadedQwen3."""
+    from accelerate import init_empty_weights
+    from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeRotaryEmbedding
+
+    from .runtime import build_offloaded_qwen3, register_tree_attention
+
+    device = torch.device(device)
+    cfg = dict(QWEN3_30B_A3B_MODEL, num_hidden_layers=layers)
+    config = Qwen3MoeConfig(**cfg)
+    config._attn_implementation = register_tree_attention()
+    with init_empty_weights():
+        model = Qwen3MoeForCausalLM(config)
+    for layer in model.model.layers:
+        layer.mlp.experts = torch.nn.Identity()
+    model.to_empty(device=device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, std, generator=gen)
+    model.to(torch.bfloat16)
+    model.model.rotary_emb = Qwen3MoeRotaryEmbedding(config, device=device)
+    if experts is None:
+        experts = make_layer(seed=seed, pin_memory=True)
+    return build_offloaded_qwen3(model, device=device, slots_per_layer=slots_per_layer,
+                                 layer_experts={l: experts.experts for l in range(layers)},
+                                 expert_execution_policy=expert_execution_policy)
+
+
+def make_kv_context(config, length: int, *, device, seed: int):
+    """A DynamicCache holding ``length`` random (N(0, 1) bf16) key/value
+    positions for every layer: the committed context the tree verifies
+    against."""
+    from transformers import DynamicCache
+
+    head_dim = getattr(config, "head_dim", config.hidden_size // config.num_attention_heads)
+    shape = (1, config.num_key_value_heads, length, head_dim)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cache = DynamicCache()
+    for layer in range(config.num_hidden_layers):
+        k = torch.randn(shape, generator=gen, device=device).to(torch.bfloat16)
+        v = torch.randn(shape, generator=gen, device=device).to(torch.bfloat16)
+        cache.update(k, v, layer)
+    return cache
