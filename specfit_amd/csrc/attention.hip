@@ -14,18 +14,17 @@
 // 4 KV heads, head dim 128) the whole layer's K/V is ~2 MB: the kernel is
 // latency-bound, not HBM-bound.  One workgroup per (query, KV head) keeps the
 // G query heads of the group together so each K/V row is read once per
-// query.  Its 4 wavefronts take interleaved 64-key chunks: scores with one
-// key per lane (the query rows broadcast from LDS), an online softmax per
-// head across the wavefront, then P.V with one value row per step and the
-// head-dim elements spread over the lanes.  The four partial (max, sum,
-// accumulator) states are merged in wavefront order, so the fp32 summation
-// order is fixed and results are run-to-run identical.
+// query.  Its 8 wavefronts take interleaved 64-key chunks: scores with one
+// key per lane (the key row in registers, the query rows broadcast from
+// LDS), an online softmax per head across the wavefront, then P.V with the
+// head-dim elements spread over the lanes and the value rows of 16 keys
+// loaded together.  The eight partial (max, sum, accumulator) states are
+// merged in wavefront order, so the fp32 summation order is fixed and
+// results are run-to-run identical.
 #include "sf_common.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / SF_WAVE;
 constexpr int kChunk = SF_WAVE;  // keys per wavefront chunk
 
 struct AttnArgs {
@@ -54,16 +53,49 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// G query heads per KV head; DPL head-dim elements per lane in P.V (D <= 64*DPL).
-template <int G, int DPL>
-__global__ __launch_bounds__(kThreads) void tree_attention_kernel(const AttnArgs a) {
+// x plus the value of lane `CTRL`-permuted lane (a DPP move: no LDS).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false);
+  return x + __int_as_float(moved);
+}
+
+// Sum over aligned groups of N lanes (N = 8 or 16), every lane gets it:
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  x = dpp_add<0xB1>(x);
+  x = dpp_add<0x4E>(x);
+  x = dpp_add<0x141>(x);
+  if (N == 16) x = dpp_add<0x140>(x);
+  return x;
+}
+
+__device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = __uint_as_float(w[e] << 16);
+    f[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+
+// G query heads per KV head.  DC > 0: head dim 8*DC known at compile time
+// (every loop unrolled, a chunk's key and value loads issued together);
+// DC == 0: any head dim (multiple of 8, <= 256) read from the arguments.
+// DPL head-dim elements per lane in P.V.  NW wavefronts per workgroup.
+template <int G, int DC, int DPL, int NW>
+__global__ __launch_bounds__(NW * SF_WAVE) void tree_attention_kernel(const AttnArgs a) {
+  constexpr int kWaves = NW;
+  constexpr int kThreads = NW * SF_WAVE;
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  const int D = a.D;
+  const int D = DC > 0 ? 8 * DC : a.D;
   float* sq = smem;                                 // [G][D] scaled query rows
-  float* sp = sq + G * D;                           // [kWaves][G][kChunk] probabilities
-  float* sm = sp + kWaves * G * kChunk;             // [kWaves][G] running max
+  float* sm = sq + G * D;                           // [kWaves][G] running max
   float* sl = sm + kWaves * G;                      // [kWaves][G] running sum
-  float* sacc = sl + kWaves * G;                    // [kWaves][G][D] accumulators
+  float* sp = sl + kWaves * G;                      // [kWaves][G][kChunk] probabilities
+  float* sacc = sp;                                 // [kWaves][G][D] accumulators (after
+                                                    // the key loop, over sp)
   const int qi = blockIdx.x / a.Hkv;
   const int h = blockIdx.x - qi * a.Hkv;
   const int lane = threadIdx.x & (SF_WAVE - 1);
@@ -90,26 +122,61 @@ __global__ __launch_bounds__(kThreads) void tree_attention_kernel(const AttnArgs
   }
   float* pw = sp + wave * G * kChunk;
   const int d0 = lane * DPL;
+  // Compile-time head dim: this lane's 8 query elements of every head.
+  float qreg[DC > 0 ? G : 1][8];
+  if (DC > 0) {
+    const int dc = lane % (DC > 0 ? DC : 1);
+#pragma unroll
+    for (int j = 0; j < (DC > 0 ? G : 1); ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qreg[j][e] = sq[j * D + 8 * dc + e];
+  }
+  const bool has_d = d0 < D;
 
   for (int kb = wave * kChunk; kb < a.S; kb += kWaves * kChunk) {
-    // Scores: lane -> key kb + lane.
+    const int nkeys = min(kChunk, a.S - kb);
+    // Scores.  With the head dim known (DC > 0), DC lanes share one key: lane
+    // l holds query elements 8*(l%DC) .. +7 of every head in registers,
+    // multiplies them with its 16 B of the key row and the DC partial sums
+    // are added by a butterfly; the chunk's scores go through LDS to the
+    // one-key-per-lane layout of the softmax.  Otherwise lane -> key.
     const int key = kb + lane;
     bool ok = key < a.S;
     if (ok) ok = a.mask ? a.mask[qi * a.mask_q + key] != 0 : key <= causal_last;
     float s[G];
+    if (DC > 0) {
+      constexpr int kKeysPer = DC > 0 ? SF_WAVE / DC : 1;  // keys per instruction
+      constexpr int kIters = kChunk / kKeysPer;
+      const int kq = lane / (DC > 0 ? DC : 1);
+      const int dc = lane % (DC > 0 ? DC : 1);
+      uint4 kv[kIters];
 #pragma unroll
-    for (int j = 0; j < G; ++j) s[j] = 0.f;
-    if (ok) {
-      const uint16_t* kr = kh + key * a.k_tok;
-      for (int d = 0; d < D; d += 8) {
-        const uint4 kv = *reinterpret_cast<const uint4*>(kr + d);
+      for (int i = 0; i < kIters; ++i) {
+        const int kk = min(kb + i * kKeysPer + kq, a.S - 1);
+        kv[i] = *reinterpret_cast<const uint4*>(kh + kk * a.k_tok + 8 * dc);
+      }
+#pragma unroll
+      for (int i = 0; i < kIters; ++i) {
         float kf[8];
-        const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+        unpack8(kv[i], kf);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          kf[2 * e] = __uint_as_float(w[e] << 16);
-          kf[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+        for (int j = 0; j < G; ++j) {
+          float part = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) part = __builtin_fmaf(qreg[j][e], kf[e], part);
+          part = group_sum<(DC == 16 ? 16 : 8)>(part);
+          if (dc == 0) pw[j * kChunk + i * kKeysPer + kq] = part;
         }
+      }
+#pragma unroll
+      for (int j = 0; j < G; ++j) s[j] = pw[j * kChunk + lane];
+    } else {
+#pragma unroll
+      for (int j = 0; j < G; ++j) s[j] = 0.f;
+      const uint16_t* kr = kh + min(key, a.S - 1) * a.k_tok;
+      for (int d = 0; d < D; d += 8) {
+        float kf[8];
+        unpack8(*reinterpret_cast<const uint4*>(kr + d), kf);
 #pragma unroll
         for (int j = 0; j < G; ++j) {
           const float* qr = sq + j * D + d;
@@ -135,25 +202,39 @@ __global__ __launch_bounds__(kThreads) void tree_attention_kernel(const AttnArgs
       for (int e = 0; e < DPL; ++e) acc[j][e] *= alpha;
       pw[j * kChunk + lane] = p;
     }
-    // P.V: one value row per step, head-dim elements d0 .. d0+DPL-1 per lane.
-    const int nkeys = min(kChunk, a.S - kb);
-    if (d0 < D) {
-      for (int t = 0; t < nkeys; ++t) {
-        const uint16_t* vr = vh + (kb + t) * a.v_tok + d0;
-        float vf[DPL];
+    // P.V: head-dim elements d0 .. d0+DPL-1 per lane; the value rows of a
+    // group of 16 keys are loaded together, then accumulated.
+    if (has_d) {
+      const uint16_t* vc = vh + kb * a.v_tok + d0;
+      for (int t0 = 0; t0 < nkeys; t0 += 16) {
+        float vf[16][DPL];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) vf[e] = sf_bf16_to_f32(vr[e]);
+        for (int t = 0; t < 16; ++t) {
+          const uint16_t* vr = vc + min(t0 + t, nkeys - 1) * a.v_tok;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) vf[t][e] = sf_bf16_to_f32(vr[e]);
+        }
+        // Keys past the end carry p = 0 (and a finite repeated row).
 #pragma unroll
         for (int j = 0; j < G; ++j) {
-          const float p = pw[j * kChunk + t];
+          const float4* p4 = reinterpret_cast<const float4*>(pw + j * kChunk + t0);
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) acc[j][e] = __builtin_fmaf(p, vf[e], acc[j][e]);
+          for (int t4 = 0; t4 < 4; ++t4) {
+            const float4 p = p4[t4];
+            const float pp[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+              for (int e = 0; e < DPL; ++e)
+                acc[j][e] = __builtin_fmaf(pp[u], vf[4 * t4 + u][e], acc[j][e]);
+          }
         }
       }
     }
   }
 
   // Merge the wavefront states in wavefront order.
+  __syncthreads();  // every wavefront is done with sp, which sacc overlays
   if (lane == 0) {
 #pragma unroll
     for (int j = 0; j < G; ++j) {
@@ -161,7 +242,7 @@ __global__ __launch_bounds__(kThreads) void tree_attention_kernel(const AttnArgs
       sl[wave * G + j] = l[j];
     }
   }
-  if (d0 < D) {
+  if (has_d) {
 #pragma unroll
     for (int j = 0; j < G; ++j)
 #pragma unroll
@@ -191,25 +272,36 @@ __global__ __launch_bounds__(kThreads) void tree_attention_kernel(const AttnArgs
   }
 }
 
-// LDS bytes of one workgroup: query rows, chunk probabilities, merge state.
+// Wavefronts per workgroup: 8 up to 8 heads per group, 4 for 16 (LDS).
+constexpr int waves_for(int G) { return G <= 8 ? 8 : 4; }
+
+// LDS bytes of one workgroup: query rows, merge state, and the larger of
+// the chunk probabilities and the merge accumulators.
 size_t lds_bytes(int G, int D) {
-  return sizeof(float) * (static_cast<size_t>(G) * D + kWaves * G * kChunk + 2 * kWaves * G +
-                          static_cast<size_t>(kWaves) * G * D);
+  const size_t w = waves_for(G);
+  const size_t shared = w * G * (D > kChunk ? D : kChunk);
+  return sizeof(float) * (static_cast<size_t>(G) * D + 2 * w * G + shared);
 }
 
 constexpr size_t kMaxLds = 64 * 1024;
 
 template <int G>
 int launch_g(const AttnArgs& a, hipStream_t s) {
-  const int dpl = (a.D + SF_WAVE - 1) / SF_WAVE;
+  constexpr int NW = waves_for(G);
   const size_t lds = lds_bytes(G, a.D);
   const dim3 grid(static_cast<unsigned>(a.Q) * a.Hkv);
-  if (dpl == 1)
-    tree_attention_kernel<G, 1><<<grid, kThreads, lds, s>>>(a);
-  else if (dpl == 2)
-    tree_attention_kernel<G, 2><<<grid, kThreads, lds, s>>>(a);
+  const dim3 block(NW * SF_WAVE);
+  // Fixed head dims 64 / 128 up to 8 heads per group (more would spill).
+  if (G <= 8 && a.D == 128)
+    tree_attention_kernel<G, (G <= 8 ? 16 : 0), 2, NW><<<grid, block, lds, s>>>(a);
+  else if (G <= 8 && a.D == 64)
+    tree_attention_kernel<G, (G <= 8 ? 8 : 0), 1, NW><<<grid, block, lds, s>>>(a);
+  else if (a.D <= SF_WAVE)
+    tree_attention_kernel<G, 0, 1, NW><<<grid, block, lds, s>>>(a);
+  else if (a.D <= 2 * SF_WAVE)
+    tree_attention_kernel<G, 0, 2, NW><<<grid, block, lds, s>>>(a);
   else
-    tree_attention_kernel<G, 4><<<grid, kThreads, lds, s>>>(a);
+    tree_attention_kernel<G, 0, 4, NW><<<grid, block, lds, s>>>(a);
   SF_LAUNCH_CHECK();
   return SF_OK;
 }

@@ -134,7 +134,8 @@ def summarize(fetch_dir: str, write_dir: str, command: str | None = None) -> str
     return "\n".join(lines) + "\n"
 
 
-def summarize_trace(trace_dir: str, command: str | None = None) -> str:
+def summarize_trace(trace_dir: str, command: str | None = None,
+                    title: str = "Qwen3-30B-A3B MoE layer, 64 tree tokens, 24-slot cache") -> str:
     """Kernel statistics of a ``rocprofv3 --kernel-trace --stats`` run of
     bench.py, with the K3 launch (gate/up + down pair) averages split into
     the in-step and all-resident phases at the calibration kernel."""
@@ -146,8 +147,7 @@ def summarize_trace(trace_dir: str, command: str | None = None) -> str:
         stats = list(csv.DictReader(fh))
     with open(trace_files[0], newline="") as fh:
         trace = sorted(csv.DictReader(fh), key=lambda r: int(r["Start_Timestamp"]))
-    lines = ["# rocprofv3 kernel statistics — Qwen3-30B-A3B MoE layer, 64 tree tokens, "
-             "24-slot cache", ""]
+    lines = [f"# rocprofv3 kernel statistics — {title}", ""]
     if command:
         lines += ["Command (run from /tmp with TMPDIR=/tmp; `<repo>` is the repository root):", "",
                   "    " + command.replace("\n", "\n    "), ""]
@@ -188,9 +188,11 @@ def main(argv=None) -> int:
     p.add_argument("--trace", help="rocprofv3 output dir of a --kernel-trace --stats run")
     p.add_argument("--command", default=None, help="command lines to quote in the summary")
     p.add_argument("--out", default=None, help="write the markdown here (default: stdout)")
+    p.add_argument("--title", default=None, help="workload named in the trace summary's title")
     args = p.parse_args(argv)
     if args.trace:
-        text = summarize_trace(args.trace, args.command)
+        text = (summarize_trace(args.trace, args.command, args.title) if args.title
+                else summarize_trace(args.trace, args.command))
     else:
         if not (args.fetch and args.write):
             p.error("--fetch and --write (or --trace) are required")
