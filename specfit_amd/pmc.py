@@ -135,7 +135,8 @@ def summarize(fetch_dir: str, write_dir: str, command: str | None = None) -> str
 
 
 def summarize_trace(trace_dir: str, command: str | None = None,
-                    title: str = "Qwen3-30B-A3B MoE layer, 64 tree tokens, 24-slot cache") -> str:
+                    title: str = "Qwen3-30B-A3B MoE layer, 64 tree tokens, 24-slot cache",
+                    split: bool = True) -> str:
     """Kernel statistics of a ``rocprofv3 --kernel-trace --stats`` run of
     bench.py, with the K3 launch (gate/up + down pair) averages split into
     the in-step and all-resident phases at the calibration kernel."""
@@ -167,8 +168,10 @@ def summarize_trace(trace_dir: str, command: str | None = None,
     lines += ["", "## K3 launches (gate/up + down dispatch pairs)", "",
               "| phase | launches | avg gate/up µs | avg down µs | avg launch µs (sum) | "
               "avg weight MB | GB/s (weights / kernel time) |", "|---|---|---|---|---|---|---|"]
-    for label, sel in (("in-step", [r for i, r in k3 if cal and i < cal[0]]),
-                       ("all-resident", [r for i, r in k3 if cal and i > cal[-1]])):
+    phases = ((("in-step", [r for i, r in k3 if cal and i < cal[0]]),
+               ("all-resident", [r for i, r in k3 if cal and i > cal[-1]])) if split
+              else (("all", [r for _, r in k3]),))
+    for label, sel in phases:
         g = [r for r in sel if "gateup" in r["Kernel_Name"]]
         d = [r for r in sel if "down_mfma" in r["Kernel_Name"]]
         if not g or len(g) != len(d):
@@ -189,10 +192,13 @@ def main(argv=None) -> int:
     p.add_argument("--command", default=None, help="command lines to quote in the summary")
     p.add_argument("--out", default=None, help="write the markdown here (default: stdout)")
     p.add_argument("--title", default=None, help="workload named in the trace summary's title")
+    p.add_argument("--no-split", action="store_true",
+                   help="one K3 row over the whole trace (workloads without the calibration "
+                        "kernel between phases)")
     args = p.parse_args(argv)
     if args.trace:
-        text = (summarize_trace(args.trace, args.command, args.title) if args.title
-                else summarize_trace(args.trace, args.command))
+        kw = {"title": args.title} if args.title else {}
+        text = summarize_trace(args.trace, args.command, split=not args.no_split, **kw)
     else:
         if not (args.fetch and args.write):
             p.error("--fetch and --write (or --trace) are required")
