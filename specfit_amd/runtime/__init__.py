@@ -9,8 +9,8 @@ from .lease import ExpertCacheStats, ExpertLease, NoEvictableSlotError
 from .qwen3_offloaded_experts import (ExpertExecutionPolicy, Qwen3OffloadedExperts,
                                       ReductionMode)
 from .qwen3_expert_prefetch import Qwen3ExpertPrefetch
-from .qwen3_offloaded_model import (LoadedOffloadedQwen3, Qwen3LoadTimings, build_offloaded_qwen3,
-                                    load_offloaded_qwen3)
+from .qwen3_offloaded_model import (LoadedOffloadedQwen3, PackedExpertBackingMode,
+                                    Qwen3LoadTimings, build_offloaded_qwen3, load_offloaded_qwen3)
 from .qwen3_router import Qwen3MoeTopKRouterHip
 from .state import ExpertKey
 from .trace import RuntimeEventKind
@@ -22,7 +22,7 @@ __all__ = [
     "CacheSlotSnapshot", "CacheTransition", "CacheTransitionCounters",
     "CacheTransitionObserver", "ExpertCacheStats", "ExpertExecutionPolicy", "ExpertKey",
     "ExpertLease", "GpuExpertCache", "GpuExpertCacheSnapshot", "NoEvictableSlotError",
-    "LoadedOffloadedQwen3", "PendingTransferSnapshot", "Qwen3ExpertPrefetch", "Qwen3LoadTimings",
+    "LoadedOffloadedQwen3", "PackedExpertBackingMode", "PendingTransferSnapshot", "Qwen3ExpertPrefetch", "Qwen3LoadTimings",
     "Qwen3MoeTopKRouterHip", "Qwen3OffloadedExperts", "build_offloaded_qwen3",
     "load_offloaded_qwen3",
     "RecordingCacheTransitionObserver", "ReductionMode", "RuntimeEventKind",

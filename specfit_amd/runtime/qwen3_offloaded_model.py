@@ -21,6 +21,7 @@ import logging
 import re
 import time
 from dataclasses import dataclass
+from enum import Enum
 from pathlib import Path
 
 import torch
@@ -35,16 +36,41 @@ from .state import ExpertKey
 _LOG = logging.getLogger(__name__)
 
 
-@dataclass(frozen=True)
-class Qwen3LoadTimings:
-    """Wall time of the load stages (seconds) and bytes moved."""
+class PackedExpertBackingMode(str, Enum):
+    """How a packed-v1 checkpoint's expert layers become pinned sources
+    (qwen3_offloaded_model.py:46-49).  Both are served by reading each layer
+    file straight into page-locked memory here: registering an existing file
+    mapping with the runtime is not available on this platform, so
+    REGISTERED_MMAP maps no file and registers nothing (its mapped and
+    registered byte counts stay 0)."""
 
+    PINNED_COPY = "pinned_copy"
+    REGISTERED_MMAP = "registered_mmap"
+
+
+@dataclass(frozen=True, slots=True)
+class Qwen3LoadTimings:
+    """Wall time of the load stages (seconds) and bytes moved; the
+    reference's fields (qwen3_offloaded_model.py:52-73)."""
+
+    checkpoint_format: str = "original"
+    expert_backing_mode: str = "original_pinned_copy"
+    checkpoint_inspection_seconds: float = 0.0
+    model_initialization_seconds: float = 0.0
+    expert_pinned_allocation_seconds: float = 0.0
+    expert_weight_read_seconds: float = 0.0
+    expert_mmap_seconds: float = 0.0
+    expert_host_registration_seconds: float = 0.0
+    expert_view_seconds: float = 0.0
+    expert_cache_initialization_seconds: float = 0.0
+    nonexpert_read_seconds: float = 0.0
+    nonexpert_h2d_seconds: float = 0.0
+    finalization_seconds: float = 0.0
     total_seconds: float = 0.0
-    expert_pack_seconds: float = 0.0
-    expert_cache_seconds: float = 0.0
-    nonexpert_seconds: float = 0.0
-    expert_bytes: int = 0
-    nonexpert_bytes: int = 0
+    expert_bytes_read: int = 0
+    expert_bytes_mapped: int = 0
+    expert_bytes_registered: int = 0
+    nonexpert_bytes_read: int = 0
 
 
 @dataclass
@@ -213,17 +239,28 @@ def _install(model, *, layer_packed: dict[int, torch.Tensor], device: torch.devi
 
 
 def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
+                         packed_checkpoint_root=None,
+                         packed_expert_backing: PackedExpertBackingMode | str | None = None,
+                         verify_packed_hashes: bool = False,
                          reduction_mode=ReductionMode.CANONICAL,
                          expert_execution_policy=ExpertExecutionPolicy.EXPERT_ID_ASCENDING,
                          attn_implementation: str = "sdpa",
                          cache_observer: CacheTransitionObserver | None = None,
                          h2d_prefetch: bool = True) -> LoadedOffloadedQwen3:
-    """Load a Qwen3-MoE checkpoint directory with offloaded experts."""
+    """Load a Qwen3-MoE checkpoint with offloaded experts
+    (qwen3_offloaded_model.py:667-840).  ``model_root`` holds config.json
+    and the original safetensors (per-expert or fused expert tensors); with
+    ``packed_checkpoint_root`` the experts and non-experts come from that
+    packed-v1 checkpoint instead, validated against ``model_root``'s
+    config/index hashes (the weight shards need not exist)."""
     from accelerate import init_empty_weights
     from safetensors import safe_open
     from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
 
+    from ..checkpoint import PackedQwen3Checkpoint, read_expert_layer_pinned
+
     start = time.perf_counter()
+    t = {}
     if type(h2d_prefetch) is not bool:
         raise ValueError("h2d_prefetch must be a boolean")
     policy = ExpertExecutionPolicy(expert_execution_policy)
@@ -232,55 +269,90 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
         raise ValueError("offloaded Qwen3 requires a CUDA device")
     if device.index is None:
         device = torch.device("cuda", torch.cuda.current_device())
-    if slots_per_layer <= 0:
-        raise ValueError("slots_per_layer must be positive")
     root = Path(model_root).resolve()
+    if packed_expert_backing is None:
+        mode = (PackedExpertBackingMode.REGISTERED_MMAP if packed_checkpoint_root is not None
+                else PackedExpertBackingMode.PINNED_COPY)
+    else:
+        mode = PackedExpertBackingMode(packed_expert_backing)
+    if packed_checkpoint_root is None and mode is not PackedExpertBackingMode.PINNED_COPY:
+        raise ValueError("registered_mmap requires packed_checkpoint_root")
     config = Qwen3MoeConfig.from_pretrained(root, local_files_only=True)
     config._attn_implementation = attn_implementation
-    files = _tensor_files(root)
     E, H, I = config.num_experts, config.hidden_size, config.moe_intermediate_size
+    if not 1 <= slots_per_layer <= E:
+        raise ValueError(f"slots_per_layer must be in [1, {E}]")
 
     handles: dict[Path, object] = {}
 
-    def get(name: str) -> torch.Tensor:
+    def get(name: str, files: dict) -> torch.Tensor:
         path = files[name]
         if path not in handles:
             handles[path] = safe_open(str(path), framework="pt")
         return handles[path].get_tensor(name)
 
-    expert_names: dict[int, dict] = {}
-    nonexpert: list[str] = []
-    for name in files:
-        m = _PER_EXPERT.match(name)
-        f = _FUSED.match(name)
-        if m or f:
-            layer = int(_LAYER.search(name).group(1))
-            entry = expert_names.setdefault(layer, {})
-            if m:
-                entry[(int(m.group(2)), m.group(3))] = name
+    t0 = time.perf_counter()
+    layer_packed: dict[int, torch.Tensor] = {}
+    if packed_checkpoint_root is not None:
+        packed = PackedQwen3Checkpoint.open(packed_checkpoint_root, source_metadata_root=root,
+                                            verify_hashes=verify_packed_hashes)
+        census = packed.census
+        if (census.num_hidden_layers, census.num_experts, census.hidden_size,
+                census.moe_intermediate_size) != (config.num_hidden_layers, E, H, I):
+            raise ValueError("packed checkpoint census does not match the model config")
+        with safe_open(str(packed.nonexpert_path), framework="pt") as h:
+            nonexpert_files = {name: packed.nonexpert_path for name in h.keys()}
+        t["checkpoint_inspection_seconds"] = time.perf_counter() - t0
+        fmt = "packed-v1"
+        read_s = 0.0
+        read_bytes = 0
+        t1 = time.perf_counter()
+        for lid in range(census.num_hidden_layers):
+            tensor, seconds = read_expert_layer_pinned(packed.layer_path(lid),
+                                                       (E, packed.packed_expert_elements))
+            layer_packed[lid] = tensor
+            read_s += seconds
+            read_bytes += tensor.numel() * tensor.element_size()
+        t["expert_weight_read_seconds"] = read_s
+        t["expert_pinned_allocation_seconds"] = time.perf_counter() - t1 - read_s
+        t["expert_bytes_read"] = read_bytes
+    else:
+        files = _tensor_files(root)
+        expert_names: dict[int, dict] = {}
+        nonexpert_files = {}
+        for name, path in files.items():
+            m = _PER_EXPERT.match(name)
+            f = _FUSED.match(name)
+            if m or f:
+                entry = expert_names.setdefault(int(_LAYER.search(name).group(1)), {})
+                if m:
+                    entry[(int(m.group(2)), m.group(3))] = name
+                else:
+                    entry[f.group(2)] = name
             else:
-                entry[f.group(2)] = name
-        else:
-            nonexpert.append(name)
-    if sorted(expert_names) != list(range(config.num_hidden_layers)):
-        raise ValueError("checkpoint does not hold routed experts for every decoder layer")
+                nonexpert_files[name] = path
+        if sorted(expert_names) != list(range(config.num_hidden_layers)):
+            raise ValueError("checkpoint does not hold routed experts for every decoder layer")
+        t["checkpoint_inspection_seconds"] = time.perf_counter() - t0
+        fmt = "original"
+        t1 = time.perf_counter()
+        layer_packed = {lid: _pack_layer_experts(lambda n: get(n, files), names, E, H, I)
+                        for lid, names in expert_names.items()}
+        t["expert_weight_read_seconds"] = time.perf_counter() - t1
+        t["expert_bytes_read"] = sum(p.numel() * 2 for p in layer_packed.values())
 
-    t_pack = time.perf_counter()
-    layer_packed = {lid: _pack_layer_experts(get, names, E, H, I)
-                    for lid, names in expert_names.items()}
-    pack_seconds = time.perf_counter() - t_pack
-
+    t2 = time.perf_counter()
     with init_empty_weights():
         model = Qwen3MoeForCausalLM(config)
-    t_non = time.perf_counter()
-    state = {}
-    nonexpert_bytes = 0
-    for name in nonexpert:
-        tensor = get(name)
-        nonexpert_bytes += tensor.numel() * tensor.element_size()
-        state[name] = tensor.to(device=device, dtype=torch.bfloat16)
     for layer in model.model.layers:
         layer.mlp.experts = torch.nn.Identity()
+    t["model_initialization_seconds"] = time.perf_counter() - t2
+    t3 = time.perf_counter()
+    host = {name: get(name, nonexpert_files) for name in nonexpert_files}
+    t["nonexpert_read_seconds"] = time.perf_counter() - t3
+    t["nonexpert_bytes_read"] = sum(v.numel() * v.element_size() for v in host.values())
+    t4 = time.perf_counter()
+    state = {name: v.to(device=device, dtype=torch.bfloat16) for name, v in host.items()}
     missing, unexpected = model.load_state_dict(state, strict=False, assign=True)
     if unexpected:
         raise ValueError(f"unexpected checkpoint tensors: {unexpected[:5]}")
@@ -288,13 +360,15 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
         model.tie_weights()
     handles.clear()
     model.model.rotary_emb.to(device)
-    nonexpert_seconds = time.perf_counter() - t_non
-    t_cache = time.perf_counter()
+    torch.cuda.synchronize(device)
+    t["nonexpert_h2d_seconds"] = time.perf_counter() - t4
+    t5 = time.perf_counter()
     caches = _install(model, layer_packed=layer_packed, device=device,
                       slots_per_layer=slots_per_layer, reduction_mode=reduction_mode,
                       expert_execution_policy=policy, h2d_prefetch=h2d_prefetch,
                       cache_observer=cache_observer)
-    cache_seconds = time.perf_counter() - t_cache
+    t["expert_cache_initialization_seconds"] = time.perf_counter() - t5
+    t6 = time.perf_counter()
     meta = [n for n, p in model.named_parameters() if p.is_meta]
     if meta:
         for cache in reversed(caches):
@@ -303,12 +377,11 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
     model.requires_grad_(False)
     model.eval()
     torch.cuda.synchronize(device)
-    timings = Qwen3LoadTimings(total_seconds=time.perf_counter() - start,
-                               expert_pack_seconds=pack_seconds,
-                               expert_cache_seconds=cache_seconds,
-                               nonexpert_seconds=nonexpert_seconds,
-                               expert_bytes=sum(p.numel() * 2 for p in layer_packed.values()),
-                               nonexpert_bytes=nonexpert_bytes)
+    t["finalization_seconds"] = time.perf_counter() - t6
+    timings = Qwen3LoadTimings(
+        checkpoint_format=fmt,
+        expert_backing_mode=mode.value if fmt == "packed-v1" else "original_pinned_copy",
+        total_seconds=time.perf_counter() - start, **t)
     _LOG.info("offloaded Qwen3 loaded: %s", timings)
     return LoadedOffloadedQwen3(model=model, expert_caches=caches, load_timings=timings)
 

@@ -8,6 +8,7 @@ cuBLAS kernels), this build compares within the MoE tolerance: its expert
 GEMMs and combine are different kernels.
 """
 import json
+from enum import Enum
 import tempfile
 from contextlib import ExitStack
 from pathlib import Path
@@ -133,17 +134,21 @@ def test_grouped_routes_noncontiguous_repeated_and_empty(device):
 def test_real_misses_start_before_ready_experts_and_ready_work_precedes_wait(device):
     loaded, _, inputs = _case(slots=4, layers=1)
     cache = loaded.expert_caches[0]
-    # One untraced forward first so first-use work (code-object loads, pinned
-    # staging allocation) cannot synchronise the device inside the window
-    # that the sleep below holds the copy stream for.
+    # Untraced forwards first, with and without a scheduler, so first-use
+    # work (code-object loads, allocator growth, pinned staging) cannot
+    # synchronise the device inside the window that the sleep below holds
+    # the copy stream for.
     loaded.model(*inputs)
+    with loaded.prefetch_experts({}):
+        loaded.model(*inputs)
+    torch.cuda.synchronize()
     loaded.cold_reset_expert_caches()
     for e in (3, 4):
         with cache.acquire(ExpertKey(0, e)) as lease:
             lease.wait()
     torch.cuda.synchronize()
     with torch.cuda.stream(cache.copy_stream):
-        torch.cuda._sleep(200_000_000)
+        torch.cuda._sleep(500_000_000)
     with loaded.prefetch_experts({}, trace=True) as sched:
         loaded.model(*inputs)
     events = sched.events()
@@ -407,8 +412,10 @@ def _save_qwen3_style_checkpoint(model, root):
             out[name] = tensor.contiguous()
     shard = "model-00001-of-00001.safetensors"
     save_file(out, root / shard)
+    total = sum(t.numel() * t.element_size() for t in out.values())
     (root / "model.safetensors.index.json").write_text(
-        json.dumps({"metadata": {}, "weight_map": {n: shard for n in out}}), encoding="utf-8")
+        json.dumps({"metadata": {"total_size": total}, "weight_map": {n: shard for n in out}}),
+        encoding="utf-8")
 
 
 def test_loader_matches_hf_eager_and_switches_policies(device):
@@ -443,3 +450,54 @@ def test_loader_matches_hf_eager_and_switches_policies(device):
             torch.testing.assert_close(expected.float().cpu(), hf, rtol=3e-2, atol=3e-2)
         with pytest.raises(RuntimeError, match="open caches"):
             loaded.set_expert_h2d_prefetch(True)
+
+
+def test_packed_checkpoint_loads_bitwise_equal_to_original(device):
+    """Packed-v1 (qwen3_offloaded_model.py:667-840 with packed_checkpoint_root):
+    both backing modes give the original checkpoint's model bit for bit."""
+    from transformers import Qwen3MoeForCausalLM
+
+    from specfit_amd.checkpoint import PackedCheckpointError, pack_qwen3_checkpoint
+    from specfit_amd.runtime import PackedExpertBackingMode
+
+    torch.manual_seed(77)
+    source = Qwen3MoeForCausalLM(_tiny_config(2)).to(torch.bfloat16)
+    ids = torch.tensor([[1, 9, 4, 33, 17]], device=device)
+    with tempfile.TemporaryDirectory() as tmp:
+        original, packed_root = Path(tmp) / "original", Path(tmp) / "packed"
+        _save_qwen3_style_checkpoint(source, original)
+        pack_qwen3_checkpoint(original, packed_root)
+        with load_offloaded_qwen3(original, device=device, slots_per_layer=2) as loaded:
+            with torch.inference_mode():
+                expected = loaded.model(ids, use_cache=False).logits
+            assert loaded.load_timings.checkpoint_format == "original"
+        E, L, elements = 4, 2, 3 * 32 * 16
+        for mode in (None, PackedExpertBackingMode.PINNED_COPY, "registered_mmap"):
+            with load_offloaded_qwen3(original, device=device, slots_per_layer=2,
+                                      packed_checkpoint_root=packed_root,
+                                      packed_expert_backing=mode,
+                                      verify_packed_hashes=True) as loaded:
+                with torch.inference_mode():
+                    actual = loaded.model(ids, use_cache=False).logits
+                timings = loaded.load_timings
+            assert torch.equal(actual, expected), mode
+            assert timings.checkpoint_format == "packed-v1"
+            assert timings.expert_backing_mode == (mode.value if isinstance(mode, Enum)
+                                                   else mode or "registered_mmap")
+            assert timings.expert_bytes_read == L * E * elements * 2
+            assert timings.expert_bytes_registered == 0 and timings.total_seconds > 0
+        for shard in original.glob("model-*.safetensors"):
+            shard.unlink()  # the packed load needs only config + index from the source
+        with load_offloaded_qwen3(original, device=device, slots_per_layer=2,
+                                  packed_checkpoint_root=packed_root) as loaded:
+            with torch.inference_mode():
+                assert torch.equal(loaded.model(ids, use_cache=False).logits, expected)
+        with pytest.raises(ValueError, match="requires packed_checkpoint_root"):
+            load_offloaded_qwen3(original, device=device, slots_per_layer=2,
+                                 packed_expert_backing="registered_mmap")
+        config = json.loads((original / "config.json").read_text())
+        config["fixture_revision"] = 1
+        (original / "config.json").write_text(json.dumps(config))
+        with pytest.raises(PackedCheckpointError, match="config SHA256"):
+            load_offloaded_qwen3(original, device=device, slots_per_layer=2,
+                                 packed_checkpoint_root=packed_root)
