@@ -12,6 +12,9 @@ from .qwen3_expert_prefetch import Qwen3ExpertPrefetch
 from .qwen3_offloaded_model import (LoadedOffloadedQwen3, PackedExpertBackingMode,
                                     Qwen3LoadTimings, build_offloaded_qwen3, load_offloaded_qwen3)
 from .qwen3_router import Qwen3MoeTopKRouterHip
+from .replay import (ExpertAccessReplayResult, LogicalReplayError, LogicalReplayEvent,
+                     ReplayCounters, ReplaySlotState, replay_qwen3_access_cycles,
+                     replay_qwen3_accesses)
 from .state import ExpertKey
 from .trace import RuntimeEventKind
 from .tree_attention import TREE_ATTENTION, register_tree_attention, tree_attention_forward
@@ -27,6 +30,8 @@ __all__ = [
     "load_offloaded_qwen3",
     "RecordingCacheTransitionObserver", "ReductionMode", "RuntimeEventKind",
     "aggregate_cache_transition_counters",
+    "ExpertAccessReplayResult", "LogicalReplayError", "LogicalReplayEvent", "ReplayCounters",
+    "ReplaySlotState", "replay_qwen3_access_cycles", "replay_qwen3_accesses",
     "Eagle3DraftTree", "TREE_ATTENTION", "TreeVerification", "compact_tree_cache",
     "register_tree_attention", "synthetic_tree", "tree_attention_forward", "verify_draft_tree",
 ]
