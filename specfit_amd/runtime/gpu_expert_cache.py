@@ -590,6 +590,80 @@ class GpuExpertCache:
             self._record_use_guards(slot, used_streams)
             slot.active_leases -= 1
 
+    def _resident_steps(self, keys, index: int, current, stream, limit: int):
+        """Run steps ``index`` .. of the layer's one-ahead lease sequence in
+        one locked pass while both the step's expert and the next one are
+        resident: for each step exactly what the caller's per-expert
+        sequence does (acquire the expert when no lease is carried over,
+        prefetch the next expert, wait on ``stream``, release keeping the
+        slot pinned), with the same LRU touches, counters, state versions
+        and observer events in the same order.  At most ``limit`` steps.
+        Returns ([(expert_id, lease, weights)], next index, carried lease).
+        If an observer raises, the leases this call took are unwound and the
+        carried-in lease stays with the caller."""
+        out = []
+        made = []
+        sid = int(stream.cuda_stream)
+        obs = self._observer
+        with self._lock:
+            self._check_open_and_known(keys[index])
+            self._reap_completed_transfers()
+            resident = self._resident
+            n = len(keys)
+            try:
+                while index + 1 < n and len(out) < limit:
+                    key, nxt = keys[index], keys[index + 1]
+                    slot_id, next_id = resident.get(key), resident.get(nxt)
+                    if slot_id is None or next_id is None:
+                        break
+                    slot = self._slots[slot_id]
+                    if current is None:  # acquire: immediate touch
+                        if obs is not None:
+                            self._record_transition(kind=RuntimeEventKind.RESIDENT_HIT,
+                                                    expert_id=key, slot=slot)
+                        self._stats.resident_hits += 1
+                        current = self._new_lease(slot, defer_touch=False)
+                        current._ready_known = True
+                        made.append(current)
+                    # one-ahead prefetch of the next expert: deferred touch
+                    nslot = self._slots[next_id]
+                    if obs is not None:
+                        self._record_transition(kind=RuntimeEventKind.RESIDENT_HIT,
+                                                expert_id=nxt, slot=nslot)
+                    self._stats.resident_hits += 1
+                    ahead = self._new_lease(nslot, defer_touch=True)
+                    ahead._ready_known = True
+                    made.append(ahead)
+                    # wait: the ready event is complete, so no stream wait
+                    current._streams[sid] = stream
+                    if current._touch_on_wait:
+                        self._touch(slot)
+                        current._touch_on_wait = False
+                    if obs is not None:
+                        self._record_consume_wait(expert_id=key, slot_id=slot.slot_id,
+                                                  generation=current.generation,
+                                                  ready_event=current.ready_event,
+                                                  stream=stream)
+                    # release, keeping the slot pinned until its launch
+                    if obs is not None:
+                        self._record_transition(kind=RuntimeEventKind.RELEASE, expert_id=key,
+                                                slot=slot, stream_ids=(sid,))
+                    self._touch(slot)
+                    current._released = True
+                    current._unpin_pending = True
+                    out.append((key.expert_id, current, slot.tensor))
+                    current = ahead
+                    index += 1
+            except BaseException:
+                done = {id(lease) for _, lease, _ in out}
+                for _, lease, _ in out:
+                    lease._unpin()
+                for lease in made:
+                    if id(lease) not in done:
+                        lease.release()
+                raise
+        return out, index, current
+
     def _unpin_many(self, leases) -> None:
         """``_unpin`` of leases whose weights one launch read: a single use
         event per stream, recorded after that launch, guards every slot of

@@ -287,17 +287,32 @@ class Qwen3OffloadedExperts(nn.Module):
 
         ahead: ExpertLease | None = None
         ahead_missed = False
+        keys = [ExpertKey(self.layer_id, e) for e in order]
+        n = len(order)
+        index = 0
         try:
-            for index, expert_id in enumerate(order):
+            while index < n:
+                if self.h2d_prefetch and misses == 0 and not ahead_missed and index + 1 < n:
+                    # Runs of resident experts: the same lease sequence in
+                    # one locked pass (no miss can occur inside the run).
+                    steps, index, ahead = cache._resident_steps(keys, index, ahead, stream,
+                                                                _MAX_BATCH - len(batch))
+                    if steps:
+                        batch.extend(steps)
+                        if len(batch) >= _MAX_BATCH:
+                            flush()
+                        continue
+                expert_id = order[index]
+                index += 1
                 current, ahead = ahead, None
                 missed, ahead_missed = ahead_missed, False
                 if current is None:
-                    k = ExpertKey(self.layer_id, expert_id)
+                    k = keys[index - 1]
                     missed = before_acquire(k, split_resident_run=True)
                     current = cache.acquire(k)
                 try:
-                    if self.h2d_prefetch and index + 1 < len(order):
-                        nxt = ExpertKey(self.layer_id, order[index + 1])
+                    if self.h2d_prefetch and index < n:
+                        nxt = keys[index]
                         will_miss = before_acquire(nxt, split_resident_run=False)
                         try:
                             ahead = cache._prefetch(nxt)
