@@ -208,6 +208,8 @@ class DispatchPlan:
     perm_pos: torch.Tensor
     inv_perm: torch.Tensor
     host_counts: torch.Tensor | None = None
+    # Python copy of host_counts[0] (routes per expert), made with it.
+    count_list: list | None = None
 
     @property
     def counts(self) -> torch.Tensor:
@@ -233,6 +235,7 @@ class DispatchPlan:
             ev.record(torch.cuda.current_stream(self.meta.device))
             ev.synchronize()
             self.host_counts = staging
+            self.count_list = staging[0].tolist()
         return self.host_counts
 
     def active_experts(self) -> tuple[int, ...]:
@@ -304,9 +307,9 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
         s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
         start, end = rec._events(s)
     max_rows = N
-    if plan.host_counts is not None:
-        counts = plan.host_counts[0]
-        max_rows = max(1, max(int(counts[int(e)]) for e in expert_ids))
+    counts = plan.count_list
+    if counts is not None:
+        max_rows = max(1, max(counts[int(e)] for e in expert_ids))
     rc = _native.lib().sf_grouped_swiglu(
         _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
         plan.tokens, plan.top_k, hidden_size, intermediate_size, n, max_rows,
@@ -316,8 +319,8 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
     if rec is not None:
         end.record(s)
         rows = 0
-        if plan.host_counts is not None:
-            rows = int(sum(int(counts[int(e)]) for e in expert_ids))
+        if counts is not None:
+            rows = int(sum(counts[int(e)] for e in expert_ids))
         rec.k3.append((n, rows, tag, start, end))
 
 

@@ -197,6 +197,12 @@ class GpuExpertCache:
             self._reap_completed_transfers()
             return tuple(sorted(self._resident, key=self._source_order.__getitem__))
 
+    def _resident_key_set(self) -> frozenset:
+        """The resident expert ids (unordered) after reaping."""
+        with self._lock:
+            self._reap_completed_transfers()
+            return frozenset(self._resident)
+
     def is_available(self, expert_id: Hashable) -> bool:
         """True when an acquire of ``expert_id`` would not choose a victim
         (resident or already in flight)."""

@@ -136,6 +136,7 @@ class Qwen3OffloadedExperts(nn.Module):
         self.combine_fp32 = combine_fp32
         self._prediction_scheduler = None
         self._num_experts: int | None = None
+        self._keys: tuple = ()  # ExpertKey of each expert id, set with _num_experts
         # Reused pinned staging of the per-forward [counts; offsets] read
         # (allocated once: growing the pinned pool can synchronise the device).
         self._host_counts: torch.Tensor | None = None
@@ -195,6 +196,7 @@ class Qwen3OffloadedExperts(nn.Module):
             n = max(ids) + 1
             if n > 256:
                 raise ValueError("at most 256 experts per layer are supported")
+            self._keys = tuple(ExpertKey(self.layer_id, e) for e in range(n))
             self._num_experts = n
         return self._num_experts
 
@@ -287,7 +289,8 @@ class Qwen3OffloadedExperts(nn.Module):
 
         ahead: ExpertLease | None = None
         ahead_missed = False
-        keys = [ExpertKey(self.layer_id, e) for e in order]
+        all_keys = self._keys
+        keys = [all_keys[e] for e in order]
         n = len(order)
         index = 0
         try:
@@ -372,7 +375,8 @@ class Qwen3OffloadedExperts(nn.Module):
             return order
         if self.execution_policy is ExpertExecutionPolicy.EXPERT_ID_ASCENDING:
             return active_experts
-        resident = frozenset(self.cache.resident_expert_ids())
-        hits = tuple(e for e in active_experts if ExpertKey(self.layer_id, e) in resident)
-        misses = tuple(e for e in active_experts if ExpertKey(self.layer_id, e) not in resident)
+        resident = self.cache._resident_key_set()
+        keys = self._keys
+        hits = tuple(e for e in active_experts if keys[e] in resident)
+        misses = tuple(e for e in active_experts if keys[e] not in resident)
         return hits + misses
