@@ -275,10 +275,12 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
                    expert_ids: Sequence[int], expert_weights: Sequence[torch.Tensor],
                    hidden_size: int, intermediate_size: int, act: torch.Tensor,
                    out_rows: torch.Tensor, *, stream: torch.cuda.Stream | None = None,
-                   tag: str = "") -> None:
+                   tag: str = "", slot_storage: torch.Tensor | None = None) -> None:
     """Grouped SwiGLU over the dispatched rows of the listed experts (K3).
     ``expert_weights[i]`` is the packed [3*H*I] bf16 weight tensor of
-    ``expert_ids[i]`` (a cache slot)."""
+    ``expert_ids[i]`` (a cache slot).  With ``slot_storage`` (the cache's
+    [slots, 3*H*I] bf16 storage) each weight is checked to be one of its
+    rows by address arithmetic instead of tensor property checks."""
     n = len(expert_ids)
     if n != len(expert_weights):
         raise ValueError("expert_ids and expert_weights differ in length")
@@ -295,13 +297,31 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
         raise ValueError("route weights must be contiguous bf16 [tokens*top_k]")
     id_arr = (ctypes.c_int32 * n)()
     w_arr = (ctypes.c_uint64 * n)()
+    if slot_storage is not None:
+        if (slot_storage.dtype != _BF16 or slot_storage.dim() != 2
+                or slot_storage.shape[1] != numel or not slot_storage.is_contiguous()
+                or slot_storage.device != hidden.device):
+            raise ValueError(f"slot storage must be contiguous bf16 [slots, {numel}]")
+        base = slot_storage.data_ptr()
+        row_bytes = numel * 2
+        span = slot_storage.shape[0] * row_bytes
+    E = plan.num_experts
     for i, (e, w) in enumerate(zip(expert_ids, expert_weights)):
-        if not 0 <= int(e) < plan.num_experts:
+        e = int(e)
+        if not 0 <= e < E:
             raise KeyError(f"unknown expert {e}")
-        if w.dtype != _BF16 or w.numel() != numel or not w.is_contiguous() or w.device != hidden.device:
+        if slot_storage is not None:
+            ptr = w.data_ptr()
+            off = ptr - base
+            if not (0 <= off < span and off % row_bytes == 0 and w.numel() == numel):
+                raise ValueError(f"packed expert {e} is not a row of the slot storage")
+        elif (w.dtype != _BF16 or w.numel() != numel or not w.is_contiguous()
+              or w.device != hidden.device):
             raise ValueError(f"packed expert {e} must be contiguous bf16 with {numel} elements")
-        id_arr[i] = int(e)
-        w_arr[i] = w.data_ptr()
+        else:
+            ptr = w.data_ptr()
+        id_arr[i] = e
+        w_arr[i] = ptr
     rec = _recorder
     if rec is not None:
         s = stream if stream is not None else torch.cuda.current_stream(hidden.device)

@@ -73,6 +73,7 @@ class _GroupedRoutes:
     rows: torch.Tensor            # bf16 [T*K, H] scaled expert outputs
     expert_ids: Sequence[int] = ()
     tag: str = ""                 # "resident" or "miss": label of the launch
+    storage: torch.Tensor | None = None  # the cache's [slots, 3*I*H] slot storage
 
 
 def _dispatch(top_k_index: torch.Tensor, num_experts: int) -> ops.DispatchPlan:
@@ -98,7 +99,7 @@ def _expert_forward(hidden_states: torch.Tensor, packed_weights, *, hidden_size:
         return ops.expert_swiglu(hidden_states, packed_weights, hidden_size, intermediate_size)
     ops.grouped_swiglu(routes.hidden, routes.plan, routes.route_weights, routes.expert_ids,
                        packed_weights, hidden_size, intermediate_size, routes.act, routes.rows,
-                       tag=routes.tag)
+                       tag=routes.tag, slot_storage=routes.storage)
     return routes.rows
 
 
@@ -189,14 +190,15 @@ class Qwen3OffloadedExperts(nn.Module):
         """Expert count of this layer: 1 + the largest expert id among the
         cache's sources for this layer."""
         if self._num_experts is None:
-            ids = [k.expert_id for k in self.cache._sources
-                   if isinstance(k, ExpertKey) and k.layer_id == self.layer_id]
-            if not ids:
+            own = {k.expert_id: k for k in self.cache._sources
+                   if isinstance(k, ExpertKey) and k.layer_id == self.layer_id}
+            if not own:
                 raise ValueError(f"cache holds no experts of layer {self.layer_id}")
-            n = max(ids) + 1
+            n = max(own) + 1
             if n > 256:
                 raise ValueError("at most 256 experts per layer are supported")
-            self._keys = tuple(ExpertKey(self.layer_id, e) for e in range(n))
+            # The cache's own key objects: map lookups then hit by identity.
+            self._keys = tuple(own.get(e) or ExpertKey(self.layer_id, e) for e in range(n))
             self._num_experts = n
         return self._num_experts
 
@@ -225,6 +227,9 @@ class Qwen3OffloadedExperts(nn.Module):
             route_weights=top_k_weights.to(torch.bfloat16).contiguous().reshape(-1),
             act=torch.empty((T * K, self.intermediate_size), dtype=torch.bfloat16, device=dev),
             rows=torch.empty((T * K, self.hidden_size), dtype=torch.bfloat16, device=dev))
+        storage = self.cache.storage
+        if storage.dim() == 2 and storage.shape[1] == 3 * self.hidden_size * self.intermediate_size:
+            routes.storage = storage
         return routes, active
 
     def _raise_invalid_index(self, top_k_index, num_experts) -> None:
