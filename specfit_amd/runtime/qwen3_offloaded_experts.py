@@ -49,7 +49,9 @@ from .state import ExpertKey
 
 
 # Largest number of experts one K3 launch of the legacy path computes.
-_MAX_BATCH = 32
+_MAX_BATCH = 64
+# Misses share a K3 launch in groups of slot_count // _MISS_GROUP_DIVISOR.
+_MISS_GROUP_DIVISOR = 2
 
 
 class ReductionMode(str, Enum):
@@ -269,9 +271,9 @@ class Qwen3OffloadedExperts(nn.Module):
         cache = self.cache
         stream = torch.cuda.current_stream(cache.device)
         batch: list[tuple[int, ExpertLease, torch.Tensor]] = []
-        # Misses are launched in groups of about a third of the slots so the
+        # Misses are launched in groups of about half the slots so the
         # copy stream never waits for the kernel of the group being filled.
-        miss_group = max(1, cache.slot_count // 3)
+        miss_group = max(1, cache.slot_count // _MISS_GROUP_DIVISOR)
         misses = 0
 
         def flush() -> None:
