@@ -306,7 +306,14 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
         row_bytes = numel * 2
         span = slot_storage.shape[0] * row_bytes
     E = plan.num_experts
-    for i, (e, w) in enumerate(zip(expert_ids, expert_weights)):
+    pairs = zip(expert_ids, expert_weights)
+    counts = plan.count_list
+    if counts is not None and n > 1:
+        # Experts with more rows take longer: give them the first workgroups
+        # so they start first and the light ones fill in behind them.  An
+        # expert's result does not depend on its position in the launch.
+        pairs = sorted(pairs, key=lambda p: -counts[int(p[0])])
+    for i, (e, w) in enumerate(pairs):
         e = int(e)
         if not 0 <= e < E:
             raise KeyError(f"unknown expert {e}")
@@ -327,7 +334,6 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
         s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
         start, end = rec._events(s)
     max_rows = N
-    counts = plan.count_list
     if counts is not None:
         max_rows = max(1, max(counts[int(e)] for e in expert_ids))
     rc = _native.lib().sf_grouped_swiglu(
