@@ -203,6 +203,67 @@ def test_grouped_swiglu_is_independent_of_grouping(device):
     assert torch.equal(scaled, rows_all[a:b])
 
 
+def test_grouped_swiglu_single_dispatch_sync(device):
+    """Each K3 call is one dispatch whose down tiles wait on per-expert
+    counters that the call returns to zero.  Calls of every row class,
+    thirty calls in a row, calls running concurrently on two streams and the
+    slot-table form all give the rows of one-expert calls bit for bit, and
+    no wait hits its poll limit."""
+    E, T, K, H, I = 32, 128, 8, 2048, 768
+    layer = make_layer(seed=11, num_experts=E, zipf_s=1.1)
+    hidden = make_hidden(T, seed=12, zipf_fold=True)
+    h_dev, idx, w, plan, rows_all, slots = _moe_rows(device, layer, hidden, K, list(range(E)))
+    ms = [int(c) for c in plan.fetch_counts()[0]]
+    print(f"single-dispatch sync case E={E} T={T} rows per expert {ms}", flush=True)
+    assert max(ms) > 64 and 0 < min(m for m in ms if m) <= 16  # every row class occurs
+    wflat = w.reshape(-1).contiguous()
+    act = torch.empty((T * K, I), dtype=torch.bfloat16, device=device)
+    ref = torch.zeros_like(rows_all)
+    active = [e for e in range(E) if ms[e]]
+    for e in active:
+        ops.grouped_swiglu(h_dev, plan, wflat, [e], [slots[e]], H, I, act, ref)
+    torch.cuda.synchronize()
+    assert torch.equal(ref, rows_all)
+    offs = plan.fetch_counts()[1]
+
+    def rows_of(experts):
+        return torch.cat([torch.arange(int(offs[e]), int(offs[e + 1]), device=device)
+                          for e in experts])
+
+    for lo, hi in ((1, 16), (17, 32), (33, 64), (65, T * K)):
+        sel = [e for e in active if lo <= ms[e] <= hi]
+        if not sel:
+            continue
+        out = torch.zeros_like(rows_all)
+        ops.grouped_swiglu(h_dev, plan, wflat, sel, [slots[e] for e in sel], H, I, act, out)
+        torch.cuda.synchronize()
+        r = rows_of(sel)
+        assert torch.equal(out[r], ref[r]), (lo, hi)
+    side = torch.cuda.Stream(device)
+    main = torch.cuda.current_stream(device)
+    outs = [torch.zeros_like(rows_all) for _ in range(30)]
+    acts = [torch.empty_like(act) for _ in range(30)]
+    torch.cuda.synchronize()
+    for i in range(30):
+        with torch.cuda.stream(side if i % 3 == 2 else main):
+            ops.grouped_swiglu(h_dev, plan, wflat, active, [slots[e] for e in active], H, I,
+                               acts[i], outs[i])
+    torch.cuda.synchronize()
+    for i, out in enumerate(outs):
+        assert torch.equal(out, ref), i
+    table = torch.arange(E, dtype=torch.int32, device=device)
+    table[::4] = -1
+    out = torch.zeros_like(rows_all)
+    ops.grouped_swiglu_table(h_dev, plan, wflat, table, slots, H, I, act, out)
+    torch.cuda.synchronize()
+    with_slot = [e for e in active if e % 4]
+    r = rows_of(with_slot)
+    assert torch.equal(out[r], ref[r])
+    r0 = rows_of([e for e in active if e % 4 == 0])
+    assert not out[r0].any()
+    assert ops.swiglu_capped_waits() == 0
+
+
 @pytest.mark.parametrize("H,I,m", [(4, 3, 2), (32, 16, 5), (96, 64, 70), (2048, 768, 130)])
 def test_expert_swiglu_generic_and_mfma_paths(device, H, I, m):
     g = torch.Generator("cpu").manual_seed(H + I + m)

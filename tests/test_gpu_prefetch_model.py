@@ -12,6 +12,7 @@ from enum import Enum
 import tempfile
 from contextlib import ExitStack
 from pathlib import Path
+import time
 from types import MappingProxyType, SimpleNamespace
 from unittest.mock import patch
 
@@ -19,6 +20,7 @@ import pytest
 import torch
 from torch import nn
 
+from specfit_amd import ops
 from specfit_amd.runtime import (ExpertKey, GpuExpertCache, LoadedOffloadedQwen3,
                                  Qwen3OffloadedExperts, RecordingCacheTransitionObserver,
                                  RuntimeEventKind, load_offloaded_qwen3)
@@ -136,8 +138,7 @@ def test_real_misses_start_before_ready_experts_and_ready_work_precedes_wait(dev
     cache = loaded.expert_caches[0]
     # Untraced forwards first, with and without a scheduler, so first-use
     # work (code-object loads, allocator growth, pinned staging) cannot
-    # synchronise the device inside the window that the sleep below holds
-    # the copy stream for.
+    # synchronise the device while the copies below are held back.
     loaded.model(*inputs)
     with loaded.prefetch_experts({}):
         loaded.model(*inputs)
@@ -147,14 +148,31 @@ def test_real_misses_start_before_ready_experts_and_ready_work_precedes_wait(dev
         with cache.acquire(ExpertKey(0, e)) as lease:
             lease.wait()
     torch.cuda.synchronize()
-    with torch.cuda.stream(cache.copy_stream):
-        torch.cuda._sleep(500_000_000)
-    with loaded.prefetch_experts({}, trace=True) as sched:
-        loaded.model(*inputs)
+    # Hold the copy stream from the first miss submission on (after the
+    # dispatch read of the forward): a stream can share a hardware queue with
+    # the compute stream, so a sleep queued earlier could also hold the
+    # dispatch.  The scheduler's choices are host-side event queries and
+    # never wait on the compute stream.
+    real_copy = ops.copy_h2d
+    held = []
+
+    def held_copy(dst, src, stream):
+        if not held:
+            with torch.cuda.stream(stream):
+                torch.cuda._sleep(500_000_000)
+            held.append(stream)
+        return real_copy(dst, src, stream)
+
+    t0 = time.perf_counter()
+    with patch.object(ops, "copy_h2d", held_copy):
+        with loaded.prefetch_experts({}, trace=True) as sched:
+            loaded.model(*inputs)
     events = sched.events()
+    print(f"scheduled forward {1e3 * (time.perf_counter() - t0):.1f} ms: "
+          f"{[(e['action'], e.get('expert_id'), e.get('waited')) for e in events]}", flush=True)
     copies = [e for e in events if e["action"] == "copy"]
     computed = [e for e in events if e["action"] == "compute"]
-    assert copies[0]["sequence"] < computed[0]["sequence"]
+    assert held and copies[0]["sequence"] < computed[0]["sequence"]
     assert [e["expert_id"] for e in computed[:2]] == [3, 4]
     assert all(not e["waited"] for e in computed[:2])
     assert {e["expert_id"] for e in computed} == set(range(5))
