@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 4
+#define SF_ABI_VERSION 3
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -127,7 +127,7 @@ int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
  *                   computes every row; with a value below some expert's
  *                   row count that expert's fp32 summation order is the one
  *                   of a smaller expert.
- * The MFMA kernel covers the Qwen3-30B-A3B expert shape (hidden 2048,
+ * The MFMA kernels cover the Qwen3-30B-A3B expert shape (hidden 2048,
  * intermediate 768) with 16-byte aligned buffers; other shapes run fp32
  * loop kernels with the same rounding points.  The fp32 summation order of
  * an output depends on the shape and on its expert's row count only.
@@ -137,27 +137,16 @@ int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
  *   act_workspace   bf16 [tokens * top_k, intermediate_size] scratch
  *   out_rows        bf16 [tokens * top_k, hidden_size] (rows of listed
  *                   experts are written, others untouched)
- *   sync_workspace  device int32 [SF_SWIGLU_SYNC_WORDS(groups)], groups =
- *                   min(n_experts, 128): the counters through which the
- *                   down tiles of an expert wait for its gate/up tiles
- *                   inside the single dispatch.  Zero-filled before its
- *                   first use; every call leaves words 0-1 and 4.. at zero
- *                   again.  Word 2 counts waits that hit their poll limit
- *                   (never expected; results of such a call are wrong).
- *                   Calls that may run concurrently need distinct
- *                   workspaces (one per stream).
  * Experts of one call are independent; the result of an expert does not
  * depend on which other experts share the call.
  */
-#define SF_SWIGLU_SYNC_WORDS(groups) (4 + (groups))
 int sf_grouped_swiglu(const void *hidden, const int32_t *perm_pos,
                       const int32_t *offsets, const void *route_weights,
                       int tokens, int top_k, int hidden_size,
                       int intermediate_size, int n_experts, int max_rows,
                       const int32_t *expert_ids,
                       const uint64_t *expert_weights, void *act_workspace,
-                      void *out_rows, int32_t *sync_workspace,
-                      sf_stream_t stream);
+                      void *out_rows, sf_stream_t stream);
 
 /*
  * K3, device slot-table form: computes every expert e < num_experts whose
@@ -165,7 +154,6 @@ int sf_grouped_swiglu(const void *hidden, const int32_t *perm_pos,
  * at slot_base + slot_of_expert[e] * slot_stride_elems (bf16 elements).
  * slot_of_expert is a device int32 [num_experts] array.  Needs no host-side
  * knowledge of which experts are active (no device-to-host read).
- * sync_workspace: SF_SWIGLU_SYNC_WORDS(num_experts) words, as above.
  */
 int sf_grouped_swiglu_table(const void *hidden, const int32_t *perm_pos,
                             const int32_t *offsets, const void *route_weights,
@@ -174,18 +162,17 @@ int sf_grouped_swiglu_table(const void *hidden, const int32_t *perm_pos,
                             const int32_t *slot_of_expert,
                             const void *slot_base, int64_t slot_stride_elems,
                             void *act_workspace, void *out_rows,
-                            int32_t *sync_workspace, sf_stream_t stream);
+                            sf_stream_t stream);
 
 /*
  * K3 on already-gathered rows of one expert (the _expert_forward seam,
  * qwen3_offloaded_experts.py:38-62): out[m, H] = y without weight scale.
  *   rows bf16 [m, hidden_size] (row stride row_stride elements)
- *   sync_workspace  SF_SWIGLU_SYNC_WORDS(1) words, as for sf_grouped_swiglu
  */
 int sf_expert_swiglu(const void *rows, int m, int64_t row_stride,
                      int hidden_size, int intermediate_size,
                      const void *packed_weights, void *act_workspace,
-                     void *out, int32_t *sync_workspace, sf_stream_t stream);
+                     void *out, sf_stream_t stream);
 
 /*
  * K4: weighted combine.  Replaces zeros_like + index_add_ of the expert

@@ -9,46 +9,35 @@
 // element is used m times and the GEMMs are bound by streaming the 9 MiB of
 // expert weights from HBM.  Every weight byte is read from HBM once.
 //
-// One dispatch per call.  Its workgroups take roles in the order they start
-// (a ticket from an atomic counter): the first groups * I/16 tickets are
-// gate/up tiles (16 activation columns of one expert), the rest are down
-// tiles (32 output columns of one expert).  A down tile loads its whole
-// weight slab into registers first, then waits until every gate/up tile of
-// its expert has published its activations (a per-expert counter with
-// agent-scope release/acquire), so down weights stream while gate/up tiles
-// still run.  A down tile only exists once every gate/up ticket has been
-// handed out, i.e. once every gate/up tile is running; gate/up tiles never
-// wait, so every wait ends.  Each wait is also capped (kSpinLimit polls);
-// a capped wait is counted in the sync workspace.  The workgroup that
-// finishes last returns the counters to zero for the next call.
-//
-// Weight stream.  A tile owns a slab of 32 weight rows (gate/up: 16 gate +
-// 16 up rows; down: 32 rows of D) and streams it in blocks of 256 k.  A
-// block is loaded row-contiguously (2 rows x 512 B per wavefront
-// instruction, ~6.2 TB/s on MI355X, where loading MFMA B fragments directly
-// touches 16 rows x 64 B per instruction and streams at ~4.4 TB/s) into
-// registers ahead of use, then written to one of two row-padded LDS tiles
-// (16 B of padding per row keeps the fragment reads conflict-free) and read
-// back as MFMA B fragments.  Token rows (the A operand, L2 resident) are
-// loaded straight into registers.  The block count is a compile-time
-// constant of the expert shape, so the loop is unrolled and every load is
-// unconditional: the compiler's vector-memory wait counts are then exact
-// (they are in-order counters; a conditional load would force a full
-// drain).  Scheduling barriers keep the loads in issue order, so registers
-// hold exactly the blocks in flight.
+// Weight stream.  A workgroup owns a slab of 32 weight rows (phase 1: the
+// 16 gate + 16 up rows of 16 activation columns; phase 2: 32 rows of D, i.e.
+// 32 output columns) and streams it in blocks of 256 k.  A block is loaded
+// row-contiguously (2 rows x 512 B per wavefront instruction, ~6.2 TB/s on
+// MI355X, where loading MFMA B fragments directly touches 16 rows x 64 B per
+// instruction and streams at ~4.4 TB/s), two blocks ahead into registers,
+// then written to one of two row-padded LDS tiles (16 B of padding per row
+// keeps the fragment reads conflict-free) and read back as MFMA B fragments.
+// Token rows (the A operand, a few KiB, L2 resident) are loaded straight into
+// registers two blocks ahead, each block's right after the MFMAs that used
+// the previous contents.  The block count is a compile-time constant of the
+// expert shape, so the loop is unrolled and every load is unconditional: the
+// compiler's vector-memory wait counts are then exact (they are in-order
+// counters; a conditional load would force a full drain).  Scheduling
+// barriers keep the loads in issue order, so registers hold only the blocks
+// in flight.
 //
 // Work split of a pass.  The 4 wavefronts cover TM sixteen-row token tiles x
 // KS k-slices (TM * KS = 4), chosen per workgroup from its expert's row
-// count m: m <= 16 -> 1 x 4, m <= 32 -> 2 x 2, larger -> 4 x 1 (and two tiles
-// per wavefront, 128 rows per pass, for experts above 64 rows).  K-slice
-// partial sums are added in LDS in slice order.  So the fp32 summation order
-// of an output depends only on (H, I) and the expert's own m, never on the
-// call, its grouping or its other experts.  Kernels are built per row class
-// (max_rows <= 16 / 32 / 64 / more) so that a call whose experts are all
-// small runs with the registers of the small split.  Rows past the end of a
-// pass repeat the pass's last row: an MFMA output row depends only on its
-// own A row and such rows are never stored, so loads need no per-lane
-// branches.
+// count m: m <= 16 -> 1 x 4, m <= 32 -> 2 x 2, larger -> 4 x 1 (two tiles per
+// wavefront, 128 rows per pass, for experts above 64 rows).  K-slice partial
+// sums are added in LDS in slice order.  So the fp32 summation order of an
+// output depends only on (H, I) and the expert's own m, never on the launch,
+// its grouping or its other experts.  The kernels are built per row class
+// (the launch's largest expert has <= 16 / 32 / 64 / more rows), so a launch
+// of small experts runs with the registers of the small split and more
+// workgroups per CU.  Rows past the end of a pass repeat the pass's last
+// row: an MFMA output row depends only on its own A row and such rows are
+// never stored, so loads need no per-lane branches.
 // MFMA: v_mfma_f32_16x16x32_bf16, A = token rows (M), B = weight rows (N).
 #include "sf_common.h"
 
@@ -57,19 +46,10 @@ namespace {
 constexpr int kMaxListExperts = 128;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / SF_WAVE;
-constexpr int kGateCols = 16;          // activation columns per gate/up tile
-constexpr int kDownCols = 32;          // output columns per down tile
-constexpr int kSlabRows = 32;          // weight rows per tile (both roles)
+constexpr int kGateCols = 16;          // activation columns per phase-1 workgroup
+constexpr int kDownCols = 32;          // output columns per phase-2 workgroup
 constexpr int kBlockK = 256;           // k per staged weight block
 constexpr int kRowBytes = kBlockK * 2 + 16;  // padded LDS row (bytes)
-
-// Sync workspace (int32 words): ticket, finished, capped waits, spare, then
-// one ready counter per group.
-constexpr int kSyncTicket = 0;
-constexpr int kSyncFinished = 1;
-constexpr int kSyncCapped = 2;
-constexpr int kSyncReady = 4;
-constexpr int kSpinLimit = 1 << 18;
 
 enum class Resolve { kList, kTable, kDense };
 
@@ -80,13 +60,12 @@ struct SwigluArgs {
   const uint16_t* route_w;  // nullptr: no routing-weight scale
   uint16_t* act;
   uint16_t* out;
-  int32_t* sync;
   int64_t row_stride;  // elements between consecutive hidden rows
   int top_k;
   int H;
   int I;
   int dense_m;
-  int n;  // groups of the launch: list length, number of experts (table), 1 (dense)
+  int n;  // list length (list/dense) or number of experts (table)
   const int32_t* slot_of_expert;
   const uint16_t* slot_base;
   int64_t slot_stride;
@@ -147,36 +126,41 @@ __device__ __forceinline__ sf_f32x4 mfma16(uint4 a, uint4 b, sf_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
-// Keeps the compiler's scheduler from moving instructions across this point
-// (loads stay in issue order, so their registers hold only blocks in flight).
-#define SF_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 // ------------------------------------------------------ streaming core --
 constexpr int kSteps = kBlockK / 32;  // MFMA k-steps per block
-constexpr int kTile = kSlabRows * kRowBytes;
+constexpr int kDepth = 2;             // blocks in flight ahead of the one in use
 
-// A weight slab of 32 rows: rows 16g .. 16g+15 start at group[g] and are
-// `stride` elements apart.
+// Keeps the compiler's scheduler from moving instructions across this point,
+// so loads stay in issue order and registers hold only blocks in flight.
+#define SF_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// A weight slab: rows 16g .. 16g+15 start at group[g] and are `stride`
+// elements apart.
+template <int NT>
 struct Slab {
-  const uint16_t* group[2];
+  const uint16_t* group[NT];
   int64_t stride;
 };
 
-// Lane l of wavefront w loads 16 B of slab rows 8i + 2w + l/32 (i < 4) at
+// Lane l of wavefront w loads 16 B of slab rows 8i + 2w + l/32 (i < 2*NT) at
 // k 8*(l%32) of block b.
-__device__ __forceinline__ void load_w(const Slab& w, int b, int lane, int wave, uint4 (&r)[4]) {
+template <int NT>
+__device__ __forceinline__ void load_w(const Slab<NT>& w, int b, int lane, int wave,
+                                       uint4 (&r)[2 * NT]) {
   const int col = b * kBlockK + (lane & 31) * 8;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2 * NT; ++i) {
     const int row = 8 * (i & 1) + 2 * wave + (lane >> 5);
     r[i] = ld16(w.group[i >> 1] + static_cast<int64_t>(row) * w.stride + col);
   }
 }
 
-__device__ __forceinline__ void store_w(char* tile, int lane, int wave, const uint4 (&r)[4]) {
+template <int NT>
+__device__ __forceinline__ void store_w(char* tile, int lane, int wave, const uint4 (&r)[2 * NT]) {
   const int colb = (lane & 31) * 16;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2 * NT; ++i) {
     const int row = 8 * i + 2 * wave + (lane >> 5);
     *reinterpret_cast<uint4*>(tile + row * kRowBytes + colb) = r[i];
   }
@@ -199,73 +183,66 @@ __device__ __forceinline__ void load_x(const uint16_t* const (&xr)[MTW], int b, 
     for (int s = 0; s < SP; ++s) x[mt][s] = ld16(xr[mt] + b * kBlockK + (s0 + s) * 32);
 }
 
-// MFMAs of one block: B fragments are read two k-steps ahead of their MFMAs
-// (the scheduling barrier keeps a group's LDS reads together, so their
+// MFMAs of one block: B fragments are read in groups ahead of their MFMAs
+// (the scheduling barrier keeps the group's LDS reads together, so their
 // latency is paid once per group).
-template <int MTW, int SP>
+template <int NT, int MTW, int SP>
 __device__ __forceinline__ void mfma_block(const char* tile, int s0, const uint4 (&x)[MTW][SP],
-                                           int lane, sf_f32x4 (&acc)[MTW][2]) {
+                                           int lane, sf_f32x4 (&acc)[MTW][NT]) {
   constexpr int kGroup = 2 < SP ? 2 : SP;
 #pragma unroll
   for (int g = 0; g < SP; g += kGroup) {
-    uint4 f[kGroup][2];
+    uint4 f[kGroup][NT];
 #pragma unroll
     for (int s = 0; s < kGroup; ++s)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) f[s][nt] = frag_b(tile, 16 * nt, s0 + g + s, lane);
+      for (int nt = 0; nt < NT; ++nt) f[s][nt] = frag_b(tile, 16 * nt, s0 + g + s, lane);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < kGroup; ++s)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int mt = 0; mt < MTW; ++mt) acc[mt][nt] = mfma16(x[mt][g + s], f[s][nt], acc[mt][nt]);
   }
 }
 
-// Weight blocks in flight ahead of the one in use (gate/up), per split:
-// small splits have registers to spare for a deeper pipeline.
-template <int MTW, int KS>
-constexpr int gateup_depth() {
-  return KS == 4 ? 4 : KS == 2 ? 3 : 2;
-}
-
-// acc = X . W^T for the gate/up slab over k-slice `slice` of KS (SP =
-// kSteps/KS k-steps of each of the NB blocks), DEPTH blocks in flight.
-// active: wave-uniform, false when the wavefront's tiles have no rows (its A
-// loads then hit one cache line, see a_rows).
-template <int MTW, int KS, int NB, int DEPTH>
-__device__ __forceinline__ void stream_gemm(const Slab& w, const uint16_t* const (&xr)[MTW],
+// acc = X . W^T over k-slice `slice` of KS (SP = kSteps/KS k-steps of each of
+// the NB blocks).  active: wave-uniform, false when the wavefront's tiles
+// have no rows (its A loads then hit one cache line, see a_rows).
+template <int NT, int MTW, int KS, int NB>
+__device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* const (&xr)[MTW],
                                             int slice, bool active, char* smem,
-                                            sf_f32x4 (&acc)[MTW][2]) {
-  static_assert(NB >= DEPTH, "fewer blocks than the prefetch depth");
+                                            sf_f32x4 (&acc)[MTW][NT]) {
+  static_assert(NB >= kDepth, "fewer blocks than the prefetch depth");
   constexpr int SP = kSteps / KS;
+  constexpr int kTile = 16 * NT * kRowBytes;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int s0 = slice * SP;
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-  uint4 wr[DEPTH][4];
-  uint4 xq[DEPTH][MTW][SP];
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+  uint4 wr[kDepth][2 * NT];
+  uint4 xq[kDepth][MTW][SP];
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) {
-    load_w(w, d, lane, wave, wr[d]);
+  for (int d = 0; d < kDepth; ++d) {
+    load_w<NT>(w, d, lane, wave, wr[d]);
     load_x<MTW, SP>(xr, d, s0, xq[d]);
   }
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    const int d = b % DEPTH;
+    const int d = b % kDepth;
     char* tile = smem + (b & 1) * kTile;
-    store_w(tile, lane, wave, wr[d]);
+    store_w<NT>(tile, lane, wave, wr[d]);
     SF_SCHED_FENCE();
-    if (b + DEPTH < NB) load_w(w, b + DEPTH, lane, wave, wr[d]);  // resolved at compile time
+    if (b + kDepth < NB) load_w<NT>(w, b + kDepth, lane, wave, wr[d]);
     SF_SCHED_FENCE();
     __syncthreads();  // tile b visible; tile b-1's reads are done
-    if (active) mfma_block<MTW, SP>(tile, s0, xq[d], lane, acc);
+    if (active) mfma_block<NT, MTW, SP>(tile, s0, xq[d], lane, acc);
     SF_SCHED_FENCE();
-    if (b + DEPTH < NB) load_x<MTW, SP>(xr, b + DEPTH, s0, xq[d]);
+    if (b + kDepth < NB) load_x<MTW, SP>(xr, b + kDepth, s0, xq[d]);
     SF_SCHED_FENCE();
   }
   __syncthreads();  // the tiles are free again
@@ -273,30 +250,30 @@ __device__ __forceinline__ void stream_gemm(const Slab& w, const uint16_t* const
 
 // Adds the KS k-slice partial sums of each tile in slice order, in LDS.
 // Returns true for the wavefront that holds the total (slice 0).
-template <int KS>
-__device__ __forceinline__ bool reduce_slices(sf_f32x4 (&acc)[1][2], char* smem) {
+template <int NT, int KS>
+__device__ __forceinline__ bool reduce_slices(sf_f32x4 (&acc)[1][NT], char* smem) {
   if (KS == 1) return true;
   constexpr int TM = kWaves / KS;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int t = wave % TM;
   const int q = wave / TM;
-  float* part = reinterpret_cast<float*>(smem);  // [KS][TM][2][4][64], lane-major
+  float* part = reinterpret_cast<float*>(smem);  // [KS][TM][NT][4][64], lane-major
   if (q > 0) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) part[(((q * TM + t) * 2 + nt) * 4 + i) * 64 + lane] = acc[0][nt][i];
+      for (int i = 0; i < 4; ++i) part[(((q * TM + t) * NT + nt) * 4 + i) * 64 + lane] = acc[0][nt][i];
   }
   __syncthreads();
   if (q == 0) {
 #pragma unroll
     for (int qq = 1; qq < KS; ++qq)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          acc[0][nt][i] += part[(((qq * TM + t) * 2 + nt) * 4 + i) * 64 + lane];
+          acc[0][nt][i] += part[(((qq * TM + t) * NT + nt) * 4 + i) * 64 + lane];
   }
   __syncthreads();
   return q == 0;
@@ -321,9 +298,9 @@ __device__ __forceinline__ bool a_rows(RowPtr row_of, int mp, const uint16_t* (&
   return active;
 }
 
-// ---------------------------------------------------------------- gate/up --
-// Tile: 16 activation columns c0.. of one expert = gate rows c0.. and up
-// rows I + c0.. of GU.
+// ---------------------------------------------------------------- phase 1 --
+// Workgroup: 16 activation columns c0.. of one expert = gate rows c0.. and up
+// rows I + c0.. of GU (NT = 2).
 template <Resolve R, int MTW, int KS, int NB>
 __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWork& wk, int tile,
                                             char* smem) {
@@ -333,7 +310,7 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
   const int wave = threadIdx.x / SF_WAVE;
   const int H = a.H;
   const int c0 = tile * kGateCols;
-  Slab w;
+  Slab<2> w;
   w.group[0] = wk.w + static_cast<int64_t>(c0) * H;
   w.group[1] = wk.w + static_cast<int64_t>(a.I + c0) * H;
   w.stride = H;
@@ -343,9 +320,9 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
     const bool active = a_rows<MTW, TM>(
         [&](int row) { return row_ptr<R>(a, wk.r0 + p0 + row); }, mp, xr);
     sf_f32x4 acc[MTW][2];
-    stream_gemm<MTW, KS, NB, gateup_depth<MTW, KS>()>(w, xr, wave / TM, active, smem, acc);
+    stream_gemm<2, MTW, KS, NB>(w, xr, wave / TM, active, smem, acc);
     bool owner = true;
-    if constexpr (KS > 1) owner = reduce_slices<KS>(acc, smem);
+    if constexpr (KS > 1) owner = reduce_slices<2, KS>(acc, smem);
     if (!owner) continue;
     // D layout: lane holds rows 4*(lane/16)+i, column lane%16.
 #pragma unroll
@@ -365,11 +342,17 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
   }
 }
 
-// Row class MC of the kernel: 0: m <= 16, 1: <= 32, 2: <= 64, 3: any.  An
-// expert above the class runs in passes of the class's largest split.
+// Row class MC of a build: 0: every expert of the launch has m <= 16, 1:
+// <= 32, 2: <= 64, 3: any.  An expert above its launch's class (max_rows
+// understated) runs in passes of the class's largest split.
 template <Resolve R, int MC, int NB>
-__device__ __forceinline__ void gateup_tile(const SwigluArgs& a, const ExpertWork& wk, int tile,
-                                            char* smem) {
+__global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const SwigluArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * 32 * kRowBytes];
+  const int tiles = a.I / kGateCols;
+  const int j = blockIdx.x / tiles;
+  const int tile = blockIdx.x - j * tiles;
+  ExpertWork wk;
+  if (!resolve<R>(a, j, wk)) return;
   if (MC == 0 || wk.m <= 16)
     gateup_body<R, 1, 4, NB>(a, wk, tile, smem);
   else if (MC == 1 || wk.m <= 32)
@@ -380,76 +363,32 @@ __device__ __forceinline__ void gateup_tile(const SwigluArgs& a, const ExpertWor
     gateup_body<R, 1, 1, NB>(a, wk, tile, smem);
 }
 
-// ------------------------------------------------------------------- down --
-// Thread 0 polls the expert's ready counter until every gate/up tile of the
-// expert has published (at most kSpinLimit polls), then acquires; the
-// barrier orders the other wavefronts' loads after it.
-__device__ __forceinline__ void wait_ready(int32_t* sync, int j, int target) {
-  if (threadIdx.x == 0) {
-    int32_t* ready = sync + kSyncReady + j;
-    int polls = 0;
-    while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      if (++polls > kSpinLimit) {
-        __hip_atomic_fetch_add(sync + kSyncCapped, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  }
-  __syncthreads();
-}
-
-// Tile: kDownCols output columns n0.. of one expert over the full I.  The
-// slab's NB blocks are loaded before the wait and stay in registers for
-// every pass; activation blocks are loaded DX ahead.
+// ---------------------------------------------------------------- phase 2 --
+// Workgroup: kDownCols output columns n0.. of one expert over the full I.
 template <Resolve R, int MTW, int KS, int NB>
-__device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork& wk, int j,
-                                          int tile, int ready_target, char* smem) {
+__device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork& wk, int tile,
+                                          char* smem) {
+  constexpr int NT = kDownCols / 16;
   constexpr int TM = kWaves / KS;
   constexpr int kPass = 16 * TM * MTW;
-  constexpr int SP = kSteps / KS;
-  constexpr int DX = MTW == 1 ? NB : 2;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int I = a.I;
   const int n0 = tile * kDownCols;
-  Slab w;
+  Slab<NT> w;
   const uint16_t* wd = wk.w + 2 * static_cast<int64_t>(a.I) * a.H + static_cast<int64_t>(n0) * I;
-  w.group[0] = wd;
-  w.group[1] = wd + static_cast<int64_t>(16) * I;
-  w.stride = I;
-  uint4 wr[NB][4];
 #pragma unroll
-  for (int b = 0; b < NB; ++b) load_w(w, b, lane, wave, wr[b]);
-  wait_ready(a.sync, j, ready_target);
-  const int s0 = (wave / TM) * SP;
+  for (int g = 0; g < NT; ++g) w.group[g] = wd + static_cast<int64_t>(16 * g) * I;
+  w.stride = I;
   for (int p0 = 0; p0 < wk.m; p0 += kPass) {
     const int mp = min(kPass, wk.m - p0);
     const uint16_t* ar[MTW];
     const bool active = a_rows<MTW, TM>(
         [&](int row) { return a.act + static_cast<int64_t>(wk.r0 + p0 + row) * I; }, mp, ar);
-    sf_f32x4 acc[MTW][2];
-#pragma unroll
-    for (int mt = 0; mt < MTW; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-    uint4 xq[DX][MTW][SP];
-#pragma unroll
-    for (int d = 0; d < DX; ++d) load_x<MTW, SP>(ar, d, s0, xq[d]);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      char* tile_b = smem + (b & 1) * kTile;
-      store_w(tile_b, lane, wave, wr[b]);
-      __syncthreads();  // tile b visible; tile b-1's reads are done
-      if (active) mfma_block<MTW, SP>(tile_b, s0, xq[b % DX], lane, acc);
-      SF_SCHED_FENCE();
-      if (b + DX < NB) load_x<MTW, SP>(ar, b + DX, s0, xq[b % DX]);
-      SF_SCHED_FENCE();
-    }
-    __syncthreads();  // the tiles are free again
+    sf_f32x4 acc[MTW][NT];
+    stream_gemm<NT, MTW, KS, NB>(w, ar, wave / TM, active, smem, acc);
     bool owner = true;
-    if constexpr (KS > 1) owner = reduce_slices<KS>(acc, smem);
+    if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
     if (!owner) continue;
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) {
@@ -460,7 +399,7 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
           const int r = wk.r0 + p0 + row;
           const float rw = a.route_w ? sf_bf16_to_f32(a.route_w[a.perm_pos[r]]) : 1.f;
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
+          for (int nt = 0; nt < NT; ++nt) {
             float y = sf_round_bf16(acc[mt][nt][i]);
             if (a.route_w) y = y * rw;
             a.out[static_cast<int64_t>(r) * a.H + n0 + 16 * nt + (lane & 15)] = sf_f32_to_bf16(y);
@@ -472,63 +411,21 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
 }
 
 template <Resolve R, int MC, int NB>
-__device__ __forceinline__ void down_tile(const SwigluArgs& a, const ExpertWork& wk, int j,
-                                          int tile, int ready_target, char* smem) {
-  if (MC == 0 || wk.m <= 16)
-    down_body<R, 1, 4, NB>(a, wk, j, tile, ready_target, smem);
-  else if (MC == 1 || wk.m <= 32)
-    down_body<R, 1, 2, NB>(a, wk, j, tile, ready_target, smem);
-  else if (MC == 3 && wk.m > 64)
-    down_body<R, 2, 1, NB>(a, wk, j, tile, ready_target, smem);
-  else
-    down_body<R, 1, 1, NB>(a, wk, j, tile, ready_target, smem);
-}
-
-// ------------------------------------------------------------- the launch --
-template <Resolve R, int MC, int NBG, int NBD>
-__global__ __launch_bounds__(kThreads) void swiglu_mfma_kernel(const SwigluArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kTile];
-  __shared__ int s_ticket;
-  __shared__ int s_last;
-  int32_t* const sync = a.sync;
-  if (threadIdx.x == 0)
-    s_ticket = __hip_atomic_fetch_add(sync + kSyncTicket, 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  const int t = s_ticket;
-  const int gate_tiles = a.I / kGateCols;
-  const int n_gate = a.n * gate_tiles;
+__global__ __launch_bounds__(kThreads) void down_mfma_kernel(const SwigluArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * kDownCols * kRowBytes];
+  const int tiles = a.H / kDownCols;
+  const int j = blockIdx.x / tiles;
+  const int tile = blockIdx.x - j * tiles;
   ExpertWork wk;
-  if (t < n_gate) {
-    const int j = t / gate_tiles;
-    if (resolve<R>(a, j, wk)) {
-      gateup_tile<R, MC, NBG>(a, wk, t - j * gate_tiles, smem);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // this thread's activations
-      __syncthreads();
-      if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(sync + kSyncReady + j, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
-  } else {
-    const int down_tiles = a.H / kDownCols;
-    const int u = t - n_gate;
-    const int j = u / down_tiles;
-    if (resolve<R>(a, j, wk)) down_tile<R, MC, NBD>(a, wk, j, u - j * down_tiles, gate_tiles, smem);
-  }
-  // Every workgroup has read its ticket and finished its wait before it
-  // counts itself finished, so the last one can clear the counters.
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(sync + kSyncFinished, 1, __ATOMIC_ACQ_REL,
-                                    __HIP_MEMORY_SCOPE_AGENT) == static_cast<int>(gridDim.x) - 1;
-  __syncthreads();
-  if (s_last) {
-    for (int i = threadIdx.x; i < a.n; i += kThreads)
-      __hip_atomic_store(sync + kSyncReady + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0) {
-      __hip_atomic_store(sync + kSyncTicket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(sync + kSyncFinished, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  if (!resolve<R>(a, j, wk)) return;
+  if (MC == 0 || wk.m <= 16)
+    down_body<R, 1, 4, NB>(a, wk, tile, smem);
+  else if (MC == 1 || wk.m <= 32)
+    down_body<R, 1, 2, NB>(a, wk, tile, smem);
+  else if (MC == 3 && wk.m > 64)
+    down_body<R, 2, 1, NB>(a, wk, tile, smem);
+  else
+    down_body<R, 1, 1, NB>(a, wk, tile, smem);
 }
 
 // ------------------------------------------------ generic (any shape) path --
@@ -591,30 +488,32 @@ bool mfma_shape_ok(int H, int I) {
 }
 
 template <Resolve R, int MC>
-int launch_mfma(const SwigluArgs& a, unsigned grid, hipStream_t s) {
-  swiglu_mfma_kernel<R, MC, kNbGateup, kNbDown><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+int launch_mfma(const SwigluArgs& a, long long g1, long long g2, hipStream_t s) {
+  gateup_mfma_kernel<R, MC, kNbGateup>
+      <<<dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, s>>>(a);
+  SF_LAUNCH_CHECK();
+  down_mfma_kernel<R, MC, kNbDown><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
   return SF_OK;
 }
 
 // max_rows bounds the rows of any expert of the launch; it picks the row
-// class of the kernel build.
+// class of the build.
 template <Resolve R>
-int launch(const SwigluArgs& a, bool mfma, int max_rows, hipStream_t s) {
-  if (a.n <= 0) return SF_OK;
+int launch(const SwigluArgs& a, int groups, bool mfma, int max_rows, hipStream_t s) {
+  if (groups <= 0) return SF_OK;
   if (mfma) {
-    const long long grid =
-        static_cast<long long>(a.n) * (a.I / kGateCols + a.H / kDownCols);
-    if (grid > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
-    const unsigned g = static_cast<unsigned>(grid);
-    if (max_rows <= 16) return launch_mfma<R, 0>(a, g, s);
-    if (max_rows <= 32) return launch_mfma<R, 1>(a, g, s);
-    if (max_rows <= 64) return launch_mfma<R, 2>(a, g, s);
-    return launch_mfma<R, 3>(a, g, s);
+    const long long g1 = static_cast<long long>(groups) * (a.I / kGateCols);
+    const long long g2 = static_cast<long long>(groups) * (a.H / kDownCols);
+    if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
+    if (max_rows <= 16) return launch_mfma<R, 0>(a, g1, g2, s);
+    if (max_rows <= 32) return launch_mfma<R, 1>(a, g1, g2, s);
+    if (max_rows <= 64) return launch_mfma<R, 2>(a, g1, g2, s);
+    return launch_mfma<R, 3>(a, g1, g2, s);
   }
-  gateup_generic_kernel<R><<<dim3(a.n), dim3(kThreads), 0, s>>>(a);
+  gateup_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
-  down_generic_kernel<R><<<dim3(a.n), dim3(kThreads), 0, s>>>(a);
+  down_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
   return SF_OK;
 }
@@ -634,13 +533,13 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
                                  const int32_t* expert_ids,
                                  const uint64_t* expert_weights,
                                  void* act_workspace, void* out_rows,
-                                 int32_t* sync_workspace, sf_stream_t stream) {
+                                 sf_stream_t stream) {
   int rc = check_common(tokens, top_k, hidden_size, intermediate_size);
   if (rc) return rc;
   if (n_experts < 0 || max_rows < 1) return SF_ERR_INVALID_ARGUMENT;
   if (n_experts == 0 || tokens == 0) return SF_OK;
   if (!hidden || !perm_pos || !offsets || !expert_ids || !expert_weights ||
-      !act_workspace || !out_rows || !sync_workspace)
+      !act_workspace || !out_rows)
     return SF_ERR_INVALID_ARGUMENT;
   bool mfma = mfma_shape_ok(hidden_size, intermediate_size) && aligned16(hidden) &&
               aligned16(act_workspace);
@@ -657,7 +556,6 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
     a.route_w = static_cast<const uint16_t*>(route_weights);
     a.act = static_cast<uint16_t*>(act_workspace);
     a.out = static_cast<uint16_t*>(out_rows);
-    a.sync = sync_workspace;
     a.row_stride = hidden_size;
     a.top_k = top_k;
     a.H = hidden_size;
@@ -667,7 +565,7 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
       a.expert[i] = expert_ids[base + i];
       a.wptr[i] = expert_weights[base + i];
     }
-    rc = launch<Resolve::kList>(a, mfma, max_rows, s);
+    rc = launch<Resolve::kList>(a, a.n, mfma, max_rows, s);
     if (rc) return rc;
   }
   return SF_OK;
@@ -680,13 +578,13 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
                                        const int32_t* slot_of_expert,
                                        const void* slot_base, int64_t slot_stride_elems,
                                        void* act_workspace, void* out_rows,
-                                       int32_t* sync_workspace, sf_stream_t stream) {
+                                       sf_stream_t stream) {
   int rc = check_common(tokens, top_k, hidden_size, intermediate_size);
   if (rc) return rc;
   if (num_experts < 1 || slot_stride_elems < 0) return SF_ERR_INVALID_ARGUMENT;
   if (tokens == 0) return SF_OK;
   if (!hidden || !perm_pos || !offsets || !slot_of_expert || !slot_base ||
-      !act_workspace || !out_rows || !sync_workspace)
+      !act_workspace || !out_rows)
     return SF_ERR_INVALID_ARGUMENT;
   const bool mfma = mfma_shape_ok(hidden_size, intermediate_size) && aligned16(hidden) &&
                     aligned16(act_workspace) && aligned16(slot_base) &&
@@ -698,7 +596,6 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
   a.route_w = static_cast<const uint16_t*>(route_weights);
   a.act = static_cast<uint16_t*>(act_workspace);
   a.out = static_cast<uint16_t*>(out_rows);
-  a.sync = sync_workspace;
   a.row_stride = hidden_size;
   a.top_k = top_k;
   a.H = hidden_size;
@@ -707,18 +604,18 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
   a.slot_of_expert = slot_of_expert;
   a.slot_base = static_cast<const uint16_t*>(slot_base);
   a.slot_stride = slot_stride_elems;
-  return launch<Resolve::kTable>(a, mfma, tokens * top_k, reinterpret_cast<hipStream_t>(stream));
+  return launch<Resolve::kTable>(a, num_experts, mfma, tokens * top_k,
+                                 reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int sf_expert_swiglu(const void* rows, int m, int64_t row_stride,
                                 int hidden_size, int intermediate_size,
                                 const void* packed_weights, void* act_workspace,
-                                void* out, int32_t* sync_workspace, sf_stream_t stream) {
+                                void* out, sf_stream_t stream) {
   if (m < 0 || hidden_size < 1 || intermediate_size < 1 || row_stride < hidden_size)
     return SF_ERR_INVALID_ARGUMENT;
   if (m == 0) return SF_OK;
-  if (!rows || !packed_weights || !act_workspace || !out || !sync_workspace)
-    return SF_ERR_INVALID_ARGUMENT;
+  if (!rows || !packed_weights || !act_workspace || !out) return SF_ERR_INVALID_ARGUMENT;
   const bool mfma = mfma_shape_ok(hidden_size, intermediate_size) && aligned16(rows) &&
                     (row_stride % 8 == 0) && aligned16(packed_weights) &&
                     aligned16(act_workspace);
@@ -726,7 +623,6 @@ extern "C" int sf_expert_swiglu(const void* rows, int m, int64_t row_stride,
   a.hidden = static_cast<const uint16_t*>(rows);
   a.act = static_cast<uint16_t*>(act_workspace);
   a.out = static_cast<uint16_t*>(out);
-  a.sync = sync_workspace;
   a.row_stride = row_stride;
   a.top_k = 1;
   a.H = hidden_size;
@@ -734,5 +630,5 @@ extern "C" int sf_expert_swiglu(const void* rows, int m, int64_t row_stride,
   a.dense_m = m;
   a.n = 1;
   a.wptr[0] = reinterpret_cast<uint64_t>(packed_weights);
-  return launch<Resolve::kDense>(a, mfma, m, reinterpret_cast<hipStream_t>(stream));
+  return launch<Resolve::kDense>(a, 1, mfma, m, reinterpret_cast<hipStream_t>(stream));
 }

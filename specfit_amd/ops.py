@@ -154,38 +154,6 @@ def _stream_handle(stream: torch.cuda.Stream | None, device: torch.device) -> in
     return int(s.cuda_stream)
 
 
-# K3 sync workspaces: int32 [4 + groups] per (device, stream), zero-filled
-# once; every K3 call leaves them zero again (word 2 counts waits that hit
-# their poll limit).  Calls on one stream run in order, so one workspace per
-# stream is never shared by two running calls.  Replaced workspaces are kept
-# alive: calls queued earlier may still use them.
-_SYNC_MIN_GROUPS = 128
-_sync_workspaces: dict[tuple[int, int], torch.Tensor] = {}
-_sync_retired: list[torch.Tensor] = []
-
-
-def _sync_workspace(device: torch.device, stream_handle: int, groups: int) -> int:
-    key = (device.index if device.index is not None else torch.cuda.current_device(),
-           stream_handle)
-    ws = _sync_workspaces.get(key)
-    if ws is None or ws.numel() < 4 + groups:
-        if ws is not None:
-            _sync_retired.append(ws)
-        ws = torch.zeros(4 + max(groups, _SYNC_MIN_GROUPS), dtype=torch.int32, device=device)
-        torch.cuda.synchronize(device)  # zeroed before any stream uses it
-        _sync_workspaces[key] = ws
-    return ws.data_ptr()
-
-
-def swiglu_capped_waits() -> int:
-    """Number of K3 waits that hit their poll limit, over every sync
-    workspace (synchronises).  Zero unless a K3 call computed wrong rows."""
-    total = 0
-    for ws in list(_sync_workspaces.values()) + _sync_retired:
-        total += int(ws[2].item())
-    return total
-
-
 def _require_cuda(name: str, t: torch.Tensor, dtype: torch.dtype | None = None) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a tensor")
@@ -368,12 +336,11 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
     max_rows = N
     if counts is not None:
         max_rows = max(1, max(counts[int(e)] for e in expert_ids))
-    sh = _stream_handle(stream, hidden.device)
     rc = _native.lib().sf_grouped_swiglu(
         _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
         plan.tokens, plan.top_k, hidden_size, intermediate_size, n, max_rows,
         ctypes.cast(id_arr, ctypes.c_void_p), ctypes.cast(w_arr, ctypes.c_void_p),
-        _ptr(act), _ptr(out_rows), _sync_workspace(hidden.device, sh, min(n, 128)), sh)
+        _ptr(act), _ptr(out_rows), _stream_handle(stream, hidden.device))
     _native.check(rc, "sf_grouped_swiglu")
     if rec is not None:
         end.record(s)
@@ -401,12 +368,11 @@ def grouped_swiglu_table(hidden: torch.Tensor, plan: DispatchPlan,
     N = plan.tokens * plan.top_k
     if act.shape != (N, intermediate_size) or out_rows.shape != (N, hidden_size):
         raise ValueError("workspace shapes do not match the dispatch plan")
-    sh = _stream_handle(stream, hidden.device)
     rc = _native.lib().sf_grouped_swiglu_table(
         _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
         plan.tokens, plan.top_k, hidden_size, intermediate_size, plan.num_experts,
         _ptr(slot_of_expert), _ptr(slot_storage), int(slot_storage.stride(0)),
-        _ptr(act), _ptr(out_rows), _sync_workspace(hidden.device, sh, plan.num_experts), sh)
+        _ptr(act), _ptr(out_rows), _stream_handle(stream, hidden.device))
     _native.check(rc, "sf_grouped_swiglu_table")
 
 
@@ -428,10 +394,9 @@ def expert_swiglu(rows: torch.Tensor, packed: torch.Tensor, hidden_size: int,
     if m == 0:
         return out
     act = torch.empty((m, intermediate_size), dtype=_BF16, device=rows.device)
-    sh = _stream_handle(stream, rows.device)
     rc = _native.lib().sf_expert_swiglu(_ptr(rows), m, int(rows.stride(0)), hidden_size,
                                         intermediate_size, _ptr(packed), _ptr(act), _ptr(out),
-                                        _sync_workspace(rows.device, sh, 1), sh)
+                                        _stream_handle(stream, rows.device))
     _native.check(rc, "sf_expert_swiglu")
     return out
 

@@ -28,7 +28,7 @@ from collections import defaultdict
 CALIBRATION_BYTES = 256 << 20   # read and written by the calibration kernel
 CALIBRATION_TAG = "neg"         # substring of the calibration kernel's name
 HIDDEN, INTERMEDIATE = 2048, 768
-GATEUP_COLS, DOWN_COLS, THREADS = 16, 64, 256
+GATEUP_COLS, DOWN_COLS, THREADS = 16, 32, 256
 
 
 def _rows(run_dir: str) -> list[dict]:
