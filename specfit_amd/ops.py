@@ -149,9 +149,15 @@ class record_launches:
         _recorder = None
 
 
+_current_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_handle(stream: torch.cuda.Stream | None, device: torch.device) -> int:
-    s = stream if stream is not None else torch.cuda.current_stream(device)
-    return int(s.cuda_stream)
+    if stream is not None:
+        return int(stream.cuda_stream)
+    if _current_raw_stream is not None and device.index is not None:
+        return _current_raw_stream(device.index)  # no Stream object on the hot path
+    return int(torch.cuda.current_stream(device).cuda_stream)
 
 
 def _require_cuda(name: str, t: torch.Tensor, dtype: torch.dtype | None = None) -> None:
@@ -295,8 +301,20 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
     if route_weights is not None and (route_weights.dtype != _BF16 or route_weights.numel() != N
                                       or not route_weights.is_contiguous()):
         raise ValueError("route weights must be contiguous bf16 [tokens*top_k]")
-    id_arr = (ctypes.c_int32 * n)()
-    w_arr = (ctypes.c_uint64 * n)()
+    E = plan.num_experts
+    ids = [int(e) for e in expert_ids]
+    weights = list(expert_weights)
+    counts = plan.count_list
+    if counts is not None and n > 1:
+        # Experts with more rows take longer: give them the first workgroups
+        # so they start first and the light ones fill in behind them.  An
+        # expert's result does not depend on its position in the launch.
+        order = sorted(range(n), key=lambda i: -counts[ids[i]])
+        ids = [ids[i] for i in order]
+        weights = [weights[i] for i in order]
+    for e in ids:
+        if not 0 <= e < E:
+            raise KeyError(f"unknown expert {e}")
     if slot_storage is not None:
         if (slot_storage.dtype != _BF16 or slot_storage.dim() != 2
                 or slot_storage.shape[1] != numel or not slot_storage.is_contiguous()
@@ -305,37 +323,26 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
         base = slot_storage.data_ptr()
         row_bytes = numel * 2
         span = slot_storage.shape[0] * row_bytes
-    E = plan.num_experts
-    pairs = zip(expert_ids, expert_weights)
-    counts = plan.count_list
-    if counts is not None and n > 1:
-        # Experts with more rows take longer: give them the first workgroups
-        # so they start first and the light ones fill in behind them.  An
-        # expert's result does not depend on its position in the launch.
-        pairs = sorted(pairs, key=lambda p: -counts[int(p[0])])
-    for i, (e, w) in enumerate(pairs):
-        e = int(e)
-        if not 0 <= e < E:
-            raise KeyError(f"unknown expert {e}")
-        if slot_storage is not None:
-            ptr = w.data_ptr()
+        ptrs = [w.data_ptr() for w in weights]
+        for e, w, ptr in zip(ids, weights, ptrs):
             off = ptr - base
             if not (0 <= off < span and off % row_bytes == 0 and w.numel() == numel):
                 raise ValueError(f"packed expert {e} is not a row of the slot storage")
-        elif (w.dtype != _BF16 or w.numel() != numel or not w.is_contiguous()
-              or w.device != hidden.device):
-            raise ValueError(f"packed expert {e} must be contiguous bf16 with {numel} elements")
-        else:
-            ptr = w.data_ptr()
-        id_arr[i] = e
-        w_arr[i] = ptr
+    else:
+        for e, w in zip(ids, weights):
+            if (w.dtype != _BF16 or w.numel() != numel or not w.is_contiguous()
+                    or w.device != hidden.device):
+                raise ValueError(f"packed expert {e} must be contiguous bf16 with {numel} elements")
+        ptrs = [w.data_ptr() for w in weights]
+    id_arr = (ctypes.c_int32 * n)(*ids)
+    w_arr = (ctypes.c_uint64 * n)(*ptrs)
     rec = _recorder
     if rec is not None:
         s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
         start, end = rec._events(s)
     max_rows = N
     if counts is not None:
-        max_rows = max(1, max(counts[int(e)] for e in expert_ids))
+        max_rows = max(1, max(counts[e] for e in ids))
     rc = _native.lib().sf_grouped_swiglu(
         _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
         plan.tokens, plan.top_k, hidden_size, intermediate_size, n, max_rows,

@@ -87,6 +87,31 @@ class _ExpertCacheCheckpoint:
     state_version: int
 
 
+class _Pin:
+    """What is left of a resident-run lease after its release bookkeeping:
+    the slot stays pinned (``active_leases``) until the kernels that read it
+    are enqueued; ``_unpin`` (or the cache's ``_unpin_many``) then records
+    the use guard and drops the pin."""
+
+    __slots__ = ("_cache", "expert_id", "slot_id", "generation", "_streams", "_unpin_pending")
+
+    def __init__(self, cache: "GpuExpertCache", expert_id: Hashable, slot_id: int,
+                 generation: int, streams: dict) -> None:
+        self._cache = cache
+        self.expert_id = expert_id
+        self.slot_id = slot_id
+        self.generation = generation
+        self._streams = streams
+        self._unpin_pending = True
+
+    def _unpin(self) -> None:
+        if not self._unpin_pending:
+            return
+        self._unpin_pending = False
+        self._cache._unpin(self.expert_id, self.slot_id, self.generation,
+                           tuple(self._streams.values()))
+
+
 class GpuExpertCache:
     """LRU cache of packed expert weights in HBM slots (one per layer)."""
 
@@ -614,6 +639,8 @@ class GpuExpertCache:
         with self._lock:
             self._check_open_and_known(keys[index])
             self._reap_completed_transfers()
+            if obs is None:
+                return self._resident_run_unobserved(keys, index, current, stream, sid, limit)
             resident = self._resident
             n = len(keys)
             try:
@@ -668,6 +695,86 @@ class GpuExpertCache:
                     if id(lease) not in done:
                         lease.release()
                 raise
+        return out, index, current
+
+    def _resident_run_unobserved(self, keys, index: int, current, stream, sid: int,
+                                 limit: int):
+        """``_resident_steps`` without an observer (lock held): the same
+        slot pins, LRU sequence numbers, state versions and hit counts,
+        kept in locals and written back once; the released entries are
+        ``_Pin`` records and only the lease carried out of the run is an
+        ``ExpertLease``."""
+        resident = self._resident
+        slots = self._slots
+        streams = {sid: stream}
+        out = []
+        n = len(keys)
+        seq = self._sequence
+        ver = self._state_version
+        hits = 0
+        ahead = None  # (key, slot) prefetched by the previous step, touch deferred
+        try:
+            while index + 1 < n and len(out) < limit:
+                key, nxt = keys[index], keys[index + 1]
+                slot_id, next_id = resident.get(key), resident.get(nxt)
+                if slot_id is None or next_id is None:
+                    break
+                slot = slots[slot_id]
+                carried = None
+                if ahead is not None:
+                    deferred = True
+                elif current is not None:
+                    carried, current = current, None
+                    deferred = carried._touch_on_wait
+                else:  # acquire: immediate touch
+                    hits += 1
+                    slot.active_leases += 1
+                    seq += 1
+                    ver += 1
+                    slot.last_used_sequence = seq
+                    deferred = False
+                # one-ahead prefetch of the next expert: deferred touch
+                nslot = slots[next_id]
+                hits += 1
+                nslot.active_leases += 1
+                ver += 1
+                ahead = (nxt, nslot)
+                if deferred:  # the wait's touch
+                    seq += 1
+                    ver += 1
+                    slot.last_used_sequence = seq
+                # release, keeping the slot pinned until its launch
+                seq += 1
+                ver += 1
+                slot.last_used_sequence = seq
+                if carried is not None:
+                    carried._streams[sid] = stream
+                    carried._touch_on_wait = False
+                    carried._released = True
+                    carried._unpin_pending = True
+                    pin = carried
+                else:
+                    pin = _Pin(self, key, slot_id, slot.generation, streams)
+                out.append((key.expert_id, pin, slot.tensor))
+                index += 1
+        except BaseException:
+            self._sequence, self._state_version = seq, ver
+            self._stats.resident_hits += hits
+            for _, pin, _ in out:
+                pin._unpin()
+            if ahead is not None:
+                nxt, nslot = ahead
+                ExpertLease(self, nxt, nslot.slot_id, nslot.generation, nslot.ready_event,
+                            _defer_touch=True).release()
+            raise
+        self._sequence = seq
+        self._state_version = ver
+        self._stats.resident_hits += hits
+        if ahead is not None:
+            nxt, nslot = ahead
+            current = ExpertLease(self, nxt, nslot.slot_id, nslot.generation, nslot.ready_event,
+                                  _defer_touch=True)
+            current._ready_known = True
         return out, index, current
 
     def _unpin_many(self, leases) -> None:

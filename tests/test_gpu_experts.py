@@ -313,3 +313,50 @@ def test_router_module_matches_hf_router_on_indices(device):
     same = torch.equal(lg.cpu(), hlg)
     if same:
         assert torch.equal(torch.sort(i.cpu(), dim=1).values, torch.sort(hi, dim=1).values)
+
+
+def test_batched_resident_runs_keep_the_reference_lease_sequence(device):
+    """Runs of resident experts are leased in one locked pass (a lean form
+    without an observer, a per-event form with one).  Both must leave the
+    cache exactly where the per-expert lease sequence (acquire, one-ahead
+    prefetch, wait, release) leaves it: slot contents, generations, LRU
+    sequence numbers and counters after every step, and the same output."""
+    E, H, I, K, slots = 12, 32, 16, 3, 8
+    g = torch.Generator().manual_seed(41)
+    sources = {e: (torch.randn(3 * I * H, generator=g) / 8).to(torch.bfloat16) for e in range(E)}
+
+    def stack(observer):
+        cache = GpuExpertCache({ExpertKey(0, e): t for e, t in sources.items()},
+                               slot_count=slots, device=device, observer=observer)
+        return cache, Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H,
+                                            intermediate_size=I,
+                                            execution_policy="resident_first", h2d_prefetch=True)
+
+    lean = stack(None)
+    observed = stack(RecordingCacheTransitionObserver(run_id="resident-runs"))
+    per_expert = stack(None)
+
+    def state(cache):
+        snap = cache.snapshot()
+        return (tuple((s.slot_id, s.expert_id, s.generation, s.last_used_sequence,
+                       s.active_leases) for s in snap.slots),
+                snap.lru_sequence, snap.submission_sequence, cache.stats())
+
+    for step in range(12):
+        T = int(torch.randint(1, 7, (1,), generator=g))
+        h = torch.randn(T, H, generator=g).to(torch.bfloat16).to(device)
+        idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(device)
+        w = torch.rand(T, K, generator=g).to(torch.bfloat16).to(device)
+        y_lean = lean[1](h, idx, w)
+        y_obs = observed[1](h, idx, w)
+        with patch.object(GpuExpertCache, "_resident_steps",
+                          lambda self, keys, index, current, stream, limit: ([], index, current)):
+            y_ref = per_expert[1](h, idx, w)
+        torch.cuda.synchronize()
+        print(f"resident-run step {step} T={T} stats {lean[0].stats()}", flush=True)
+        assert state(lean[0]) == state(per_expert[0]), step
+        assert state(observed[0]) == state(per_expert[0]), step
+        assert torch.equal(y_lean, y_ref) and torch.equal(y_obs, y_ref)
+    assert lean[0].stats().resident_hits > 20  # the runs were exercised
+    for cache, _ in (lean, observed, per_expert):
+        cache.close()
