@@ -138,6 +138,9 @@ class GpuExpertCache:
         items = tuple(cpu_sources.items())
         shape, dtype = items[0][1].shape, items[0][1].dtype
         self._sources: dict[Hashable, torch.Tensor] = {}
+        # Each source key maps to itself: slots, the resident and in-flight
+        # maps store these objects, so lookups with them match by identity.
+        self._canonical_keys: dict[Hashable, Hashable] = {}
         self._source_order: dict[Hashable, int] = {}
         for order, (expert_id, src) in enumerate(items):
             if src.device.type != "cpu":
@@ -155,6 +158,7 @@ class GpuExpertCache:
                 pinned.copy_(src.detach())
             self._sources[expert_id] = pinned
             self._source_order[expert_id] = order
+            self._canonical_keys[expert_id] = expert_id
 
         with torch.cuda.device(self.device):
             self.copy_stream = torch.cuda.Stream(device=self.device)
@@ -441,6 +445,7 @@ class GpuExpertCache:
                 s.ready_event = None
                 s.use_events.clear()
             self._sources.clear()
+            self._canonical_keys.clear()
             owner, self._source_owner = self._source_owner, None
             if owner is not None:
                 owner.close()
@@ -494,6 +499,7 @@ class GpuExpertCache:
         return None
 
     def _assign_and_submit(self, slot: _Slot, expert_id: Hashable) -> None:
+        expert_id = self._canonical_keys.get(expert_id, expert_id)
         victim = slot.expert_id
         if victim is not None:
             self._resident.pop(victim, None)
@@ -575,7 +581,8 @@ class GpuExpertCache:
                                 pending_use_guards=pending_use_guards)
 
     def _validate_lease(self, slot: _Slot, expert_id: Hashable, generation: int) -> None:
-        if slot.expert_id != expert_id or slot.generation != generation or slot.active_leases <= 0:
+        if ((slot.expert_id is not expert_id and slot.expert_id != expert_id)
+                or slot.generation != generation or slot.active_leases <= 0):
             raise RuntimeError("expert lease refers to a reused GPU slot")
 
     def _lease_tensor(self, expert_id: Hashable, slot_id: int, generation: int, *,

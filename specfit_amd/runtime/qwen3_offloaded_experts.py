@@ -218,10 +218,11 @@ class Qwen3OffloadedExperts(nn.Module):
         if self._host_counts is None:
             self._host_counts = torch.empty((2, num_experts + 1), dtype=torch.int32,
                                             pin_memory=True)
-        counts = plan.fetch_counts(self._host_counts)[0]
-        if int(counts[num_experts]):
+        plan.fetch_counts(self._host_counts)
+        counts = plan.count_list
+        if counts[num_experts]:
             self._raise_invalid_index(top_k_index, num_experts)
-        active = tuple(int(e) for e in torch.nonzero(counts[:num_experts]).flatten().tolist())
+        active = tuple(e for e in range(num_experts) if counts[e])
         dev = hidden_states.device
         routes = _GroupedRoutes(
             hidden=hidden_states.contiguous(),
