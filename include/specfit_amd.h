@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 3
+#define SF_ABI_VERSION 5
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -154,11 +154,13 @@ int sf_grouped_swiglu(const void *hidden, const int32_t *perm_pos,
  * at slot_base + slot_of_expert[e] * slot_stride_elems (bf16 elements).
  * slot_of_expert is a device int32 [num_experts] array.  Needs no host-side
  * knowledge of which experts are active (no device-to-host read).
+ * max_rows bounds the rows of any expert as for sf_grouped_swiglu (tokens
+ * is one when every token's top_k experts are distinct, as a router's are).
  */
 int sf_grouped_swiglu_table(const void *hidden, const int32_t *perm_pos,
                             const int32_t *offsets, const void *route_weights,
                             int tokens, int top_k, int hidden_size,
-                            int intermediate_size, int num_experts,
+                            int intermediate_size, int num_experts, int max_rows,
                             const int32_t *slot_of_expert,
                             const void *slot_base, int64_t slot_stride_elems,
                             void *act_workspace, void *out_rows,

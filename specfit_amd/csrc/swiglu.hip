@@ -574,14 +574,14 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
 extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_pos,
                                        const int32_t* offsets, const void* route_weights,
                                        int tokens, int top_k, int hidden_size,
-                                       int intermediate_size, int num_experts,
+                                       int intermediate_size, int num_experts, int max_rows,
                                        const int32_t* slot_of_expert,
                                        const void* slot_base, int64_t slot_stride_elems,
                                        void* act_workspace, void* out_rows,
                                        sf_stream_t stream) {
   int rc = check_common(tokens, top_k, hidden_size, intermediate_size);
   if (rc) return rc;
-  if (num_experts < 1 || slot_stride_elems < 0) return SF_ERR_INVALID_ARGUMENT;
+  if (num_experts < 1 || slot_stride_elems < 0 || max_rows < 1) return SF_ERR_INVALID_ARGUMENT;
   if (tokens == 0) return SF_OK;
   if (!hidden || !perm_pos || !offsets || !slot_of_expert || !slot_base ||
       !act_workspace || !out_rows)
@@ -604,7 +604,7 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
   a.slot_of_expert = slot_of_expert;
   a.slot_base = static_cast<const uint16_t*>(slot_base);
   a.slot_stride = slot_stride_elems;
-  return launch<Resolve::kTable>(a, num_experts, mfma, tokens * top_k,
+  return launch<Resolve::kTable>(a, num_experts, mfma, max_rows,
                                  reinterpret_cast<hipStream_t>(stream));
 }
 

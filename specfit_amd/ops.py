@@ -216,6 +216,7 @@ class DispatchPlan:
     host_counts: torch.Tensor | None = None
     # Python copy of host_counts[0] (routes per expert), made with it.
     count_list: list | None = None
+    _counts_event: tuple | None = None  # (event, staging) of a started read
 
     @property
     def counts(self) -> torch.Tensor:
@@ -231,15 +232,32 @@ class DispatchPlan:
         without one a pinned buffer is allocated (which may synchronise the
         device while the allocator grows, so hot paths pass one)."""
         if self.host_counts is None:
-            shape = (2, self.num_experts + 1)
-            if staging is None:
-                staging = torch.empty(shape, dtype=torch.int32, pin_memory=True)
-            elif staging.shape != shape or staging.dtype != torch.int32 or not staging.is_pinned():
-                raise ValueError("staging must be pinned int32 [2, num_experts + 1]")
-            staging.copy_(self.meta, non_blocking=True)
-            ev = torch.cuda.Event()
-            ev.record(torch.cuda.current_stream(self.meta.device))
+            self.start_counts(staging)
+        return self.finish_counts()
+
+    def start_counts(self, staging: torch.Tensor | None = None) -> None:
+        """Enqueue the [counts; offsets] copy on the current stream without
+        waiting (``finish_counts`` waits), so work enqueued after it does
+        not delay the read."""
+        if self.host_counts is not None or self._counts_event is not None:
+            return
+        shape = (2, self.num_experts + 1)
+        if staging is None:
+            staging = torch.empty(shape, dtype=torch.int32, pin_memory=True)
+        elif staging.shape != shape or staging.dtype != torch.int32 or not staging.is_pinned():
+            raise ValueError("staging must be pinned int32 [2, num_experts + 1]")
+        staging.copy_(self.meta, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.meta.device))
+        self._counts_event = (ev, staging)
+
+    def finish_counts(self) -> torch.Tensor:
+        if self.host_counts is None:
+            if self._counts_event is None:
+                self.start_counts()
+            ev, staging = self._counts_event
             ev.synchronize()
+            self._counts_event = None
             self.host_counts = staging
             self.count_list = staging[0].tolist()
         return self.host_counts
@@ -361,11 +379,16 @@ def grouped_swiglu_table(hidden: torch.Tensor, plan: DispatchPlan,
                          route_weights: torch.Tensor | None, slot_of_expert: torch.Tensor,
                          slot_storage: torch.Tensor, hidden_size: int, intermediate_size: int,
                          act: torch.Tensor, out_rows: torch.Tensor, *,
-                         stream: torch.cuda.Stream | None = None) -> None:
+                         max_rows: int | None = None, stream: torch.cuda.Stream | None = None,
+                         tag: str = "") -> list | None:
     """K3 over every expert whose device slot-table entry is >= 0 (no host
-    knowledge of the active set needed)."""
+    knowledge of the active set needed).  ``max_rows`` bounds any expert's
+    rows (default tokens * top_k; tokens when every token's experts are
+    distinct).  While launches are recorded, returns the recorder's entry
+    ``[experts, rows, tag, start, end]``: the caller fills in the first two
+    once it knows which experts had rows."""
     if plan.tokens == 0:
-        return
+        return None
     _require_cuda("slot_of_expert", slot_of_expert, torch.int32)
     if slot_of_expert.numel() != plan.num_experts or not slot_of_expert.is_contiguous():
         raise ValueError("slot_of_expert must be contiguous int32 [num_experts]")
@@ -375,12 +398,25 @@ def grouped_swiglu_table(hidden: torch.Tensor, plan: DispatchPlan,
     N = plan.tokens * plan.top_k
     if act.shape != (N, intermediate_size) or out_rows.shape != (N, hidden_size):
         raise ValueError("workspace shapes do not match the dispatch plan")
+    bound = N if max_rows is None else int(max_rows)
+    if bound < 1:
+        raise ValueError("max_rows must be positive")
+    rec = _recorder
+    entry = None
+    if rec is not None:
+        s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
+        start, end = rec._events(s)
     rc = _native.lib().sf_grouped_swiglu_table(
         _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
-        plan.tokens, plan.top_k, hidden_size, intermediate_size, plan.num_experts,
+        plan.tokens, plan.top_k, hidden_size, intermediate_size, plan.num_experts, bound,
         _ptr(slot_of_expert), _ptr(slot_storage), int(slot_storage.stride(0)),
         _ptr(act), _ptr(out_rows), _stream_handle(stream, hidden.device))
     _native.check(rc, "sf_grouped_swiglu_table")
+    if rec is not None:
+        end.record(s)
+        entry = [0, 0, tag, start, end]
+        rec.k3.append(entry)
+    return entry
 
 
 def expert_swiglu(rows: torch.Tensor, packed: torch.Tensor, hidden_size: int,

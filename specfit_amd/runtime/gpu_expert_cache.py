@@ -232,6 +232,28 @@ class GpuExpertCache:
             self._reap_completed_transfers()
             return frozenset(self._resident)
 
+    def _slot_table(self, keys) -> tuple[list[int], list[torch.cuda.Event]]:
+        """Slot of each key that is resident or in flight, -1 for the
+        others, and the ready events of the in-flight ones (a reader waits
+        on them).  Stays exact while the caller holds the lock."""
+        with self._lock:
+            self._reap_completed_transfers()
+            resident = self._resident
+            inflight = self._inflight
+            table = []
+            pending = []
+            for k in keys:
+                slot = resident.get(k)
+                if slot is None:
+                    t = inflight.get(k)
+                    if t is not None:
+                        slot = t.slot_id
+                        pending.append(t.ready_event)
+                    else:
+                        slot = -1
+                table.append(slot)
+            return table, pending
+
     def is_available(self, expert_id: Hashable) -> bool:
         """True when an acquire of ``expert_id`` would not choose a victim
         (resident or already in flight)."""

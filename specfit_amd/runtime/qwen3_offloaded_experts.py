@@ -76,6 +76,7 @@ class _GroupedRoutes:
     expert_ids: Sequence[int] = ()
     tag: str = ""                 # "resident" or "miss": label of the launch
     storage: torch.Tensor | None = None  # the cache's [slots, 3*I*H] slot storage
+    covered: frozenset = frozenset()  # experts whose rows a slot-table launch computed
 
 
 def _dispatch(top_k_index: torch.Tensor, num_experts: int) -> ops.DispatchPlan:
@@ -103,6 +104,9 @@ def _expert_forward(hidden_states: torch.Tensor, packed_weights, *, hidden_size:
                        packed_weights, hidden_size, intermediate_size, routes.act, routes.rows,
                        tag=routes.tag, slot_storage=routes.storage)
     return routes.rows
+
+
+_DEFAULT_EXPERT_FORWARD = _expert_forward
 
 
 class Qwen3OffloadedExperts(nn.Module):
@@ -143,6 +147,12 @@ class Qwen3OffloadedExperts(nn.Module):
         # Reused pinned staging of the per-forward [counts; offsets] read
         # (allocated once: growing the pinned pool can synchronise the device).
         self._host_counts: torch.Tensor | None = None
+        # Device slot table (slot of each expert id or -1) and its pinned
+        # staging, rewritten by every slot-table forward.
+        self._table_host: torch.Tensor | None = None
+        self._table_dev: torch.Tensor | None = None
+        # Whether the layer's last legacy forward copied an expert in.
+        self._last_forward_copied = True
 
     # -------------------------------------------------------------- forward --
     def forward(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
@@ -153,16 +163,100 @@ class Qwen3OffloadedExperts(nn.Module):
             if execution_order is not None:
                 raise ValueError("explicit execution_order conflicts with dynamic predicted prefetch")
             return self._forward_prefetched(hidden_states, top_k_index, top_k_weights)
+        if execution_order is None and self._uses_slot_table():
+            return self._forward_slot_table(hidden_states, top_k_index, top_k_weights)
         routes, active = self._prepare(hidden_states, top_k_index, top_k_weights)
         order = self._resolve_execution_order(active, execution_order)
         if routes is None:
             return torch.zeros_like(hidden_states)
-        self._run_in_order(order, routes)
+        self._run_legacy(order, routes)
         if self.reduction_mode is ReductionMode.ARRIVAL_ORDER:
             return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
                                expert_rank=self._arrival_ranks(order), accumulate_fp32=False)
         return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
                            accumulate_fp32=self.combine_fp32)
+
+    def _uses_slot_table(self) -> bool:
+        """The resident-first, one-ahead forward with the stock K3 seam and a
+        [slots, 3*H*I] slot storage runs its resident experts from the
+        device slot table when the layer's previous forward copied nothing
+        in.  A layer that keeps missing takes the per-launch path instead:
+        there the resident launch goes after the first miss copy is queued
+        (the copies bound the step and the kernel hides under them), while
+        the table launch would add its host cost before that copy."""
+        storage = self.cache.storage
+        return (not self._last_forward_copied
+                and self.execution_policy is ExpertExecutionPolicy.RESIDENT_FIRST
+                and self.h2d_prefetch and _expert_forward is _DEFAULT_EXPERT_FORWARD
+                and storage.dim() == 2
+                and storage.shape[1] == 3 * self.hidden_size * self.intermediate_size)
+
+    def _forward_slot_table(self, hidden_states, top_k_index, top_k_weights):
+        """Resident-first forward whose resident experts start before the
+        routes reach the host: right after K2 and the counts read it starts,
+        one K3 launch over the device slot table (the slot of every expert
+        whose copy has completed or is in flight; the launch waits for the
+        latter) computes every such expert that has rows while the host
+        waits for the counts.  Then the reference lease sequence runs unchanged
+        (resident hits, one-ahead prefetch, misses), with K3 launches only
+        for the experts the table launch did not cover: misses, transfers
+        submitted after the table was taken, and experts with more rows than
+        tokens (repeated ids in a token's routes), whose rows the table
+        launch computed with the split of a smaller expert.  Holding the
+        cache lock from the table to the end of the sequence keeps every
+        table slot in place until its lease records the use guard that
+        covers the table launch (the lease is released on the compute
+        stream after it)."""
+        T, K = top_k_index.shape
+        if hidden_states.dtype != torch.bfloat16:
+            raise ValueError("hidden_states must be bfloat16")
+        if T == 0 or K == 0:
+            return torch.zeros_like(hidden_states)
+        num_experts = self.num_experts()
+        cache = self.cache
+        with cache._lock:
+            plan = _dispatch(top_k_index, num_experts)
+            plan.start_counts(self._counts_staging(num_experts))
+            routes = self._new_routes(hidden_states, top_k_weights, plan)
+            slots, pending = cache._slot_table(self._keys)
+            stream = torch.cuda.current_stream(hidden_states.device)
+            for ready in pending:  # transfers still in flight
+                stream.wait_event(ready)
+            table = self._upload_slot_table(slots, hidden_states.device)
+            entry = ops.grouped_swiglu_table(routes.hidden, plan, routes.route_weights, table,
+                                             routes.storage, self.hidden_size,
+                                             self.intermediate_size, routes.act, routes.rows,
+                                             max_rows=T, tag="resident")
+            counts = self._read_counts(plan, top_k_index, num_experts)
+            active = tuple(e for e in range(num_experts) if counts[e])
+            routes.covered = frozenset(e for e in active if slots[e] >= 0 and counts[e] <= T)
+            if entry is not None:
+                entry[0] = len(routes.covered)
+                entry[1] = sum(counts[e] for e in routes.covered)
+            order = self._resolve_execution_order(active, None)
+            self._run_legacy(order, routes)
+        if self.reduction_mode is ReductionMode.ARRIVAL_ORDER:
+            return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
+                               expert_rank=self._arrival_ranks(order), accumulate_fp32=False)
+        return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
+                           accumulate_fp32=self.combine_fp32)
+
+    def _run_legacy(self, order, routes) -> None:
+        before = self.cache._stats.h2d_submissions
+        self._run_in_order(order, routes)
+        self._last_forward_copied = self.cache._stats.h2d_submissions != before
+
+    def _upload_slot_table(self, slots: list[int], device: torch.device) -> torch.Tensor:
+        """Copy the slot table to the device on the current stream.  The
+        pinned staging is reused: the previous forward's upload was ordered
+        before its counts read, which that forward waited for."""
+        E = len(slots)
+        if self._table_host is None or self._table_host.numel() != E:
+            self._table_host = torch.empty(E, dtype=torch.int32, pin_memory=True)
+            self._table_dev = torch.empty(E, dtype=torch.int32, device=device)
+        self._table_host.numpy()[:] = slots
+        self._table_dev.copy_(self._table_host, non_blocking=True)
+        return self._table_dev
 
     def _forward_prefetched(self, hidden_states, top_k_index, top_k_weights):
         """Scheduler-driven forward (qwen3_offloaded_experts.py:166-203): the
@@ -215,14 +309,26 @@ class Qwen3OffloadedExperts(nn.Module):
             return None, ()
         num_experts = self.num_experts()
         plan = _dispatch(top_k_index, num_experts)
+        counts = self._read_counts(plan, top_k_index, num_experts)
+        active = tuple(e for e in range(num_experts) if counts[e])
+        return self._new_routes(hidden_states, top_k_weights, plan), active
+
+    def _counts_staging(self, num_experts: int) -> torch.Tensor:
         if self._host_counts is None:
             self._host_counts = torch.empty((2, num_experts + 1), dtype=torch.int32,
                                             pin_memory=True)
-        plan.fetch_counts(self._host_counts)
+        return self._host_counts
+
+    def _read_counts(self, plan, top_k_index, num_experts) -> list:
+        """The layer's one device-to-host read: routes per expert."""
+        plan.fetch_counts(self._counts_staging(num_experts))
         counts = plan.count_list
         if counts[num_experts]:
             self._raise_invalid_index(top_k_index, num_experts)
-        active = tuple(e for e in range(num_experts) if counts[e])
+        return counts
+
+    def _new_routes(self, hidden_states, top_k_weights, plan) -> _GroupedRoutes:
+        T, K = plan.tokens, plan.top_k
         dev = hidden_states.device
         routes = _GroupedRoutes(
             hidden=hidden_states.contiguous(),
@@ -233,7 +339,7 @@ class Qwen3OffloadedExperts(nn.Module):
         storage = self.cache.storage
         if storage.dim() == 2 and storage.shape[1] == 3 * self.hidden_size * self.intermediate_size:
             routes.storage = storage
-        return routes, active
+        return routes
 
     def _raise_invalid_index(self, top_k_index, num_experts) -> None:
         values = top_k_index.flatten().tolist()
@@ -250,13 +356,19 @@ class Qwen3OffloadedExperts(nn.Module):
 
     def _launch(self, routes: _GroupedRoutes, batch: list[tuple[int, ExpertLease, torch.Tensor]],
                 tag: str = "") -> None:
-        """One K3 launch for a batch of waited leases, then unpin them."""
+        """One K3 launch for the batch's experts that a slot-table launch
+        did not already compute, then unpin every lease of the batch (the
+        use guard is recorded after both launches on the compute stream)."""
         try:
-            routes.expert_ids = [e for e, _, _ in batch]
-            routes.tag = tag
-            _expert_forward(routes.hidden, [w for _, _, w in batch],
-                            hidden_size=self.hidden_size,
-                            intermediate_size=self.intermediate_size, routes=routes)
+            covered = routes.covered
+            todo = [(e, w) for e, _, w in batch if e not in covered] if covered else \
+                [(e, w) for e, _, w in batch]
+            if todo:
+                routes.expert_ids = [e for e, _ in todo]
+                routes.tag = tag
+                _expert_forward(routes.hidden, [w for _, w in todo],
+                                hidden_size=self.hidden_size,
+                                intermediate_size=self.intermediate_size, routes=routes)
         finally:
             self.cache._unpin_many([lease for _, lease, _ in batch])
 

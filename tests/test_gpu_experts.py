@@ -16,6 +16,7 @@ from specfit_amd.runtime import (ExpertExecutionPolicy, ExpertKey, GpuExpertCach
                                  RecordingCacheTransitionObserver, ReductionMode,
                                  RuntimeEventKind)
 from specfit_amd.runtime import qwen3_offloaded_experts as implementation
+from specfit_amd import ops
 from specfit_amd.workloads import make_hidden, make_layer
 
 pytestmark = pytest.mark.gpu
@@ -360,3 +361,87 @@ def test_batched_resident_runs_keep_the_reference_lease_sequence(device):
     assert lean[0].stats().resident_hits > 20  # the runs were exercised
     for cache, _ in (lean, observed, per_expert):
         cache.close()
+
+
+@pytest.mark.parametrize("shape", ["tiny", "qwen3"])
+def test_slot_table_forward_matches_the_launch_path(device, shape):
+    """After a forward that copied nothing in, a resident-first layer runs
+    its resident experts from the device slot table.  Output bits, cache
+    slots, LRU and submission sequences and counters must equal those of
+    the per-launch path (the same order passed explicitly), also when the
+    table forward misses and when a token repeats an expert (an expert with
+    more rows than tokens)."""
+    if shape == "tiny":
+        E, H, I, K, slots = 12, 32, 16, 3, 10
+    else:
+        E, H, I, K, slots = 12, 2048, 768, 3, 10
+    g = torch.Generator().manual_seed(77)
+    sources = {e: (torch.randn(3 * I * H, generator=g) * 0.02).to(torch.bfloat16)
+               for e in range(E)}
+
+    def stack():
+        cache = GpuExpertCache({ExpertKey(0, e): t for e, t in sources.items()},
+                               slot_count=slots, device=device)
+        return cache, Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H,
+                                            intermediate_size=I,
+                                            execution_policy="resident_first", h2d_prefetch=True)
+
+    (ca, la), (cb, lb) = stack(), stack()
+
+    def state(cache):
+        snap = cache.snapshot()
+        return (tuple((s.slot_id, s.expert_id, s.generation, s.last_used_sequence)
+                      for s in snap.slots), snap.lru_sequence, snap.submission_sequence,
+                cache.stats())
+
+    def resident_ids():
+        return sorted(k.expert_id for k in cb._resident_key_set())
+
+    def from_pool(T, pool):
+        pool = torch.tensor(pool)
+        return torch.stack([pool[torch.randperm(len(pool), generator=g)[:K]] for _ in range(T)])
+
+    # (kind, tokens): load all of 0..9; resident experts only; a token that
+    # repeats an expert; one expert outside the cache (a miss)
+    steps = [("load", 4), ("resident", 5), ("resident", 6), ("repeat", 2), ("miss", 6),
+             ("resident", 5), ("resident", 7)]
+    real = ops.grouped_swiglu_table
+    table_calls = []
+
+    def spy(*args, **kwargs):
+        table_calls.append(kwargs.get("max_rows"))
+        return real(*args, **kwargs)
+
+    for step, (kind, T) in enumerate(steps):
+        if kind == "load":
+            idx = torch.tensor([[0, 1, 2], [3, 4, 5], [6, 7, 8], [9, 0, 1]])
+        elif kind == "resident":
+            idx = from_pool(T, resident_ids())
+        elif kind == "repeat":
+            r = resident_ids()
+            idx = torch.tensor([[r[0], r[0], r[1]], [r[0], r[2], r[3]]])
+        else:
+            outside = [e for e in range(E) if e not in resident_ids()]
+            idx = from_pool(T, resident_ids())
+            idx[0, 0] = outside[0]
+        h = (torch.randn(T, H, generator=g)).to(torch.bfloat16).to(device)
+        w = torch.rand(T, K, generator=g).to(torch.bfloat16).to(device)
+        idx = idx.to(device)
+        uses_table = la._uses_slot_table()
+        active = sorted(set(idx.flatten().tolist()))
+        resident = cb._resident_key_set()
+        order = ([e for e in active if ExpertKey(0, e) in resident]
+                 + [e for e in active if ExpertKey(0, e) not in resident])
+        calls = len(table_calls)
+        with patch.object(ops, "grouped_swiglu_table", spy):
+            ya = la(h, idx, w)
+        yb = lb(h, idx, w, execution_order=order)
+        torch.cuda.synchronize()
+        print(f"slot-table case {shape} step {step} T={T} table={uses_table} "
+              f"stats {ca.stats()}", flush=True)
+        assert (len(table_calls) > calls) == uses_table
+        assert torch.equal(ya, yb), step
+        assert state(ca) == state(cb), step
+    assert len(table_calls) == 4  # hits only (twice), repeated expert, a miss
+    ca.close()
+    cb.close()
