@@ -235,10 +235,12 @@ class DispatchPlan:
             self.start_counts(staging)
         return self.finish_counts()
 
-    def start_counts(self, staging: torch.Tensor | None = None) -> None:
-        """Enqueue the [counts; offsets] copy on the current stream without
-        waiting (``finish_counts`` waits), so work enqueued after it does
-        not delay the read."""
+    def start_counts(self, staging: torch.Tensor | None = None,
+                     stream: torch.cuda.Stream | None = None) -> None:
+        """Enqueue the [counts; offsets] copy without waiting
+        (``finish_counts`` waits).  With ``stream`` the copy runs there,
+        after the dispatch enqueued so far on the current stream, so work
+        enqueued later on the current stream does not delay the read."""
         if self.host_counts is not None or self._counts_event is not None:
             return
         shape = (2, self.num_experts + 1)
@@ -246,9 +248,15 @@ class DispatchPlan:
             staging = torch.empty(shape, dtype=torch.int32, pin_memory=True)
         elif staging.shape != shape or staging.dtype != torch.int32 or not staging.is_pinned():
             raise ValueError("staging must be pinned int32 [2, num_experts + 1]")
-        staging.copy_(self.meta, non_blocking=True)
         ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.meta.device))
+        if stream is None:
+            staging.copy_(self.meta, non_blocking=True)
+            ev.record(torch.cuda.current_stream(self.meta.device))
+        else:
+            stream.wait_stream(torch.cuda.current_stream(self.meta.device))
+            with torch.cuda.stream(stream):
+                staging.copy_(self.meta, non_blocking=True)
+            ev.record(stream)
         self._counts_event = (ev, staging)
 
     def finish_counts(self) -> torch.Tensor:

@@ -141,6 +141,7 @@ class GpuExpertCache:
         # Each source key maps to itself: slots, the resident and in-flight
         # maps store these objects, so lookups with them match by identity.
         self._canonical_keys: dict[Hashable, Hashable] = {}
+        self._table_version = 0  # bumped on every slot assignment, reset and restore
         self._source_order: dict[Hashable, int] = {}
         for order, (expert_id, src) in enumerate(items):
             if src.device.type != "cpu":
@@ -232,10 +233,12 @@ class GpuExpertCache:
             self._reap_completed_transfers()
             return frozenset(self._resident)
 
-    def _slot_table(self, keys) -> tuple[list[int], list[torch.cuda.Event]]:
-        """Slot of each key that is resident or in flight, -1 for the
-        others, and the ready events of the in-flight ones (a reader waits
-        on them).  Stays exact while the caller holds the lock."""
+    def _slot_table(self, keys) -> tuple[int, list[int], list[torch.cuda.Event]]:
+        """(table version, slot of each key that is resident or in flight
+        or -1, ready events of the in-flight ones: a reader waits on them).
+        The version changes whenever an expert is assigned a slot or the
+        cache is reset or restored; stays exact while the caller holds the
+        lock."""
         with self._lock:
             self._reap_completed_transfers()
             resident = self._resident
@@ -252,7 +255,7 @@ class GpuExpertCache:
                     else:
                         slot = -1
                 table.append(slot)
-            return table, pending
+            return self._table_version, table, pending
 
     def is_available(self, expert_id: Hashable) -> bool:
         """True when an acquire of ``expert_id`` would not choose a victim
@@ -381,6 +384,7 @@ class GpuExpertCache:
                 raise RuntimeError("cold reset requires explicit CUDA synchronization")
             self._resident.clear()
             self._inflight.clear()
+            self._table_version += 1
             self._outstanding_transfers.clear()
             for s in self._slots:
                 s.expert_id = None
@@ -434,6 +438,7 @@ class GpuExpertCache:
             self._slots = [replace(s, tensor=self._storage[s.slot_id], use_events=dict(s.use_events))
                            for s in checkpoint.slots]
             self._resident = dict(checkpoint.resident)
+            self._table_version += 1
             self._inflight = dict(checkpoint.inflight)
             self._outstanding_transfers = deque(checkpoint.transfers)
             self._stats = replace(checkpoint.stats)
@@ -461,6 +466,7 @@ class GpuExpertCache:
             torch.cuda.synchronize(self.device)
             self._resident.clear()
             self._inflight.clear()
+            self._table_version += 1
             self._outstanding_transfers.clear()
             for s in self._slots:
                 s.expert_id = None
@@ -522,6 +528,7 @@ class GpuExpertCache:
 
     def _assign_and_submit(self, slot: _Slot, expert_id: Hashable) -> None:
         expert_id = self._canonical_keys.get(expert_id, expert_id)
+        self._table_version += 1
         victim = slot.expert_id
         if victim is not None:
             self._resident.pop(victim, None)

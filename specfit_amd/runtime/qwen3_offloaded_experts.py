@@ -151,6 +151,7 @@ class Qwen3OffloadedExperts(nn.Module):
         # staging, rewritten by every slot-table forward.
         self._table_host: torch.Tensor | None = None
         self._table_dev: torch.Tensor | None = None
+        self._table_version: int | None = None  # cache table version on the device
         # Whether the layer's last legacy forward copied an expert in.
         self._last_forward_copied = True
 
@@ -214,15 +215,16 @@ class Qwen3OffloadedExperts(nn.Module):
             return torch.zeros_like(hidden_states)
         num_experts = self.num_experts()
         cache = self.cache
+        dev = hidden_states.device
         with cache._lock:
+            version, slots, pending = cache._slot_table(self._keys)
+            table = self._upload_slot_table(version, slots, dev)
             plan = _dispatch(top_k_index, num_experts)
             plan.start_counts(self._counts_staging(num_experts))
             routes = self._new_routes(hidden_states, top_k_weights, plan)
-            slots, pending = cache._slot_table(self._keys)
-            stream = torch.cuda.current_stream(hidden_states.device)
+            stream = torch.cuda.current_stream(dev)
             for ready in pending:  # transfers still in flight
                 stream.wait_event(ready)
-            table = self._upload_slot_table(slots, hidden_states.device)
             entry = ops.grouped_swiglu_table(routes.hidden, plan, routes.route_weights, table,
                                              routes.storage, self.hidden_size,
                                              self.intermediate_size, routes.act, routes.rows,
@@ -246,16 +248,21 @@ class Qwen3OffloadedExperts(nn.Module):
         self._run_in_order(order, routes)
         self._last_forward_copied = self.cache._stats.h2d_submissions != before
 
-    def _upload_slot_table(self, slots: list[int], device: torch.device) -> torch.Tensor:
-        """Copy the slot table to the device on the current stream.  The
-        pinned staging is reused: the previous forward's upload was ordered
-        before its counts read, which that forward waited for."""
+    def _upload_slot_table(self, version: int, slots: list[int],
+                           device: torch.device) -> torch.Tensor:
+        """Copy the slot table to the device on the current stream, unless
+        the table of this cache version is already there.  The pinned
+        staging is reused: the previous forward's upload was ordered before
+        its counts read, which that forward waited for."""
         E = len(slots)
         if self._table_host is None or self._table_host.numel() != E:
             self._table_host = torch.empty(E, dtype=torch.int32, pin_memory=True)
             self._table_dev = torch.empty(E, dtype=torch.int32, device=device)
-        self._table_host.numpy()[:] = slots
-        self._table_dev.copy_(self._table_host, non_blocking=True)
+            self._table_version = None
+        if version != self._table_version:
+            self._table_host.numpy()[:] = slots
+            self._table_dev.copy_(self._table_host, non_blocking=True)
+            self._table_version = version
         return self._table_dev
 
     def _forward_prefetched(self, hidden_states, top_k_index, top_k_weights):
