@@ -59,11 +59,11 @@ float oracle_exp_nonpos(float x) {
   return p * scale;
 }
 
-/* Combine 64 lane partials with the xor butterfly d = 32..1 and return the
- * (lane-invariant) result. */
+/* Combine 64 lane partials with the xor butterfly d = 1, 2, ..., 32 and
+ * return the (lane-invariant) result. */
 static float butterfly_sum(float *v) {
   float next[WAVE];
-  for (int d = 32; d >= 1; d >>= 1) {
+  for (int d = 1; d <= 32; d <<= 1) {
     for (int l = 0; l < WAVE; ++l) next[l] = v[l] + v[l ^ d];
     memcpy(v, next, sizeof(next));
   }

@@ -48,13 +48,33 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
       atomicAdd(&s_invalid, 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int e = 0; e < E; ++e) {
-      s_offset[e] = run;
-      run += s_total[e];
+  if (wave == 0) {
+    // Exclusive prefix of s_total over the experts: lane l owns experts
+    // 4l .. 4l+3 (SF_MAX_EXPERTS = 256 = 4 x 64), a wavefront inclusive scan
+    // of the lane sums gives each lane its starting offset.
+    constexpr int kPer = SF_MAX_EXPERTS / SF_WAVE;
+    int own[kPer];
+    int sum = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int e = lane * kPer + q;
+      own[q] = e < E ? s_total[e] : 0;
+      sum += own[q];
     }
-    s_offset[E] = run;
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < SF_WAVE; d <<= 1) {
+      const int up = __shfl_up(incl, d, SF_WAVE);
+      if (lane >= d) incl += up;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int e = lane * kPer + q;
+      if (e < E) s_offset[e] = run;
+      run += own[q];
+    }
+    if (lane == SF_WAVE - 1) s_offset[E] = incl;
   }
   __syncthreads();
   for (int e = tid; e < E; e += kDispatchThreads) {

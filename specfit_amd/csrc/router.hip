@@ -8,7 +8,7 @@
 //    hidden[k]*W[e,k] for its k in ascending order into an fp32 partial that
 //    starts at +0 (bf16*bf16 products are exact in fp32, so fused and unfused
 //    accumulation agree).  The 64 partials are combined by an xor butterfly
-//    with distances 32,16,8,4,2,1 (v[l] += v[l^d]); the result is rounded to
+//    with distances 1,2,4,8,16,32 (v[l] += v[l^d]); the result is rounded to
 //    bf16 (nearest even).
 //  * softmax: m = max logit; x_e = exp(logit_e - m) with sf_exp_nonpos; lane l
 //    owns experts l, l+64, l+128, l+192 and sums its x_e in that order from
@@ -18,24 +18,14 @@
 //    (p descending, expert id ascending).
 //  * weights: v_j / (((v_0 + v_1) + v_2) + ...) when renormalising, else v_j,
 //    rounded to bf16.
+// Wavefront reductions are DPP moves and lane reads (sf_wave_sum /
+// sf_wave_max), which give exactly these butterfly sums.
 #include "sf_common.h"
 
 namespace {
 
 constexpr int kRouterThreads = 256;
 constexpr int kRouterWaves = kRouterThreads / SF_WAVE;
-
-__device__ __forceinline__ float wave_sum_butterfly(float v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, SF_WAVE);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max_butterfly(float v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, SF_WAVE));
-  return v;
-}
 
 __device__ __forceinline__ float dot8_acc(uint4 hv, uint4 wv, float acc) {
   const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
@@ -52,22 +42,26 @@ __device__ __forceinline__ float dot8_acc(uint4 hv, uint4 wv, float acc) {
   return acc;
 }
 
-// Softmax + top-k + renorm over s_logit[0..E) by wavefront 0 of the block.
+// Softmax + top-k + renorm over s_logit[0..E) by one wavefront.  Lane l
+// reads only experts l, l+64, ... of s_logit.  Each top-k round takes the
+// wave maximum of the unselected probabilities and the lowest expert id
+// holding it (ballots per 64-expert slice, lowest lane first).
 __device__ void softmax_topk_wave(const float* s_logit, int E, int K, int renorm,
                                   uint16_t* topw, int64_t* topi, float* s_val,
                                   int* s_id) {
+  constexpr int J = SF_MAX_EXPERTS / SF_WAVE;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   float m = -__builtin_inff();
 #pragma unroll
-  for (int j = 0; j < SF_MAX_EXPERTS / SF_WAVE; ++j) {
+  for (int j = 0; j < J; ++j) {
     int e = lane + SF_WAVE * j;
     if (e < E) m = fmaxf(m, s_logit[e]);
   }
-  m = wave_max_butterfly(m);
-  float x[SF_MAX_EXPERTS / SF_WAVE];
+  m = sf_wave_max(m);
+  float x[J];
   float part = 0.0f;
 #pragma unroll
-  for (int j = 0; j < SF_MAX_EXPERTS / SF_WAVE; ++j) {
+  for (int j = 0; j < J; ++j) {
     int e = lane + SF_WAVE * j;
     if (e < E) {
       x[j] = sf_exp_nonpos(s_logit[e] - m);
@@ -76,41 +70,30 @@ __device__ void softmax_topk_wave(const float* s_logit, int E, int K, int renorm
       x[j] = 0.0f;
     }
   }
-  const float total = wave_sum_butterfly(part);
-  float p[SF_MAX_EXPERTS / SF_WAVE];
-  bool live[SF_MAX_EXPERTS / SF_WAVE];
+  const float total = sf_wave_sum(part);
+  float p[J];
+  bool live[J];
 #pragma unroll
-  for (int j = 0; j < SF_MAX_EXPERTS / SF_WAVE; ++j) {
+  for (int j = 0; j < J; ++j) {
     int e = lane + SF_WAVE * j;
     live[j] = e < E;
     p[j] = live[j] ? x[j] / total : 0.0f;
   }
   for (int r = 0; r < K; ++r) {
-    float bp = -1.0f;
+    float lb = -1.0f;  // probabilities are >= 0
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (live[j] && p[j] > lb) lb = p[j];
+    const float bp = sf_wave_max(lb);
     int be = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < SF_MAX_EXPERTS / SF_WAVE; ++j) {
-      // ids grow with j inside a lane, so a strict comparison keeps the
-      // lowest id among equal probabilities.
-      if (live[j] && p[j] > bp) {
-        bp = p[j];
-        be = lane + SF_WAVE * j;
-      }
+    for (int j = 0; j < J; ++j) {
+      const unsigned long long hit = __ballot(live[j] && p[j] == bp);
+      if (be == 0x7fffffff && hit) be = SF_WAVE * j + __ffsll(hit) - 1;
     }
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-      float op = __shfl_xor(bp, d, SF_WAVE);
-      int oe = __shfl_xor(be, d, SF_WAVE);
-      if (op > bp || (op == bp && oe < be)) {
-        bp = op;
-        be = oe;
-      }
-    }
-    if ((be & (SF_WAVE - 1)) == lane) {
-#pragma unroll
-      for (int j = 0; j < SF_MAX_EXPERTS / SF_WAVE; ++j)
-        if (be == lane + SF_WAVE * j) live[j] = false;
-    }
+    for (int j = 0; j < J; ++j)
+      if (be == lane + SF_WAVE * j) live[j] = false;
     if (lane == 0) {
       s_val[r] = bp;
       s_id[r] = be;
@@ -127,79 +110,95 @@ __device__ void softmax_topk_wave(const float* s_logit, int E, int K, int renorm
   }
 }
 
-// Vector path: hidden_size % 8 == 0, 16-byte aligned rows, and at most
-// NCH chunks of 8 elements per lane, so the token's hidden row stays in
-// registers.  Sixteen wavefronts share the experts; each takes them four at
-// a time with all router-weight loads of the four issued before any use, so
-// the block is bound by one L2 round trip per group instead of one per
-// expert.
-constexpr int kRouterVecThreads = 1024;
-constexpr int kRouterVecWaves = kRouterVecThreads / SF_WAVE;
-// Experts per group: 16 uint4 router-weight registers per lane at most.
+// Vector path: hidden_size % 8 == 0, 16-byte aligned rows and at most NCH
+// chunks of 8 elements per lane.  Two kernels, so the dot products spread
+// over the whole chip: the logits kernel gives each wavefront a tile of TT
+// tokens x EPW experts (all loads of the tile issued before any use, each
+// logit summed per lane and butterflied exactly as above), the select
+// kernel runs softmax / top-k / renormalisation with one wavefront per
+// token.
+constexpr int kLogitWaves = 4;
 template <int NCH>
-struct ExpertGroup {
-  static constexpr int value = NCH <= 4 ? 4 : (NCH <= 8 ? 2 : 1);
+struct LogitTile {
+  static constexpr int experts = NCH <= 4 ? 4 : (NCH <= 8 ? 2 : 1);  // per wavefront
+  static constexpr int tokens = NCH <= 4 ? 2 : 1;
 };
 
 template <int NCH>
-__global__ __launch_bounds__(kRouterVecThreads) void router_topk_vec_kernel(
-    const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ wr, int H,
-    int E, int K, int renorm, uint16_t* __restrict__ logits,
-    uint16_t* __restrict__ topw, int64_t* __restrict__ topi) {
-  constexpr int kExpertGroup = ExpertGroup<NCH>::value;
-  __shared__ float s_logit[SF_MAX_EXPERTS];
-  __shared__ float s_val[SF_MAX_TOPK];
-  __shared__ int s_id[SF_MAX_TOPK];
-  const int t = blockIdx.x;
+__global__ __launch_bounds__(kLogitWaves * SF_WAVE) void router_logits_kernel(
+    const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ wr, int T, int H,
+    int E, uint16_t* __restrict__ logits) {
+  constexpr int EPW = LogitTile<NCH>::experts;
+  constexpr int TT = LogitTile<NCH>::tokens;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
+  const int t0 = blockIdx.x * TT;
+  const int e0 = (blockIdx.y * kLogitWaves + wave) * EPW;
+  if (e0 >= E) return;  // wave-uniform; the kernel has no block barrier
   const int nchunks = H / 8;
-  const uint4* h4 = reinterpret_cast<const uint4*>(hidden + static_cast<size_t>(t) * H);
-  uint4 hreg[NCH];
+  uint4 hreg[TT][NCH];
+  uint4 wv[EPW][NCH];
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    int c = lane + SF_WAVE * i;
-    hreg[i] = c < nchunks ? h4[c] : make_uint4(0, 0, 0, 0);
-  }
-  for (int e0 = wave * kExpertGroup; e0 < E; e0 += kRouterVecWaves * kExpertGroup) {
-    uint4 wv[kExpertGroup][NCH];
+  for (int tt = 0; tt < TT; ++tt) {
+    const uint4* h4 =
+        reinterpret_cast<const uint4*>(hidden + static_cast<size_t>(min(t0 + tt, T - 1)) * H);
 #pragma unroll
-    for (int g = 0; g < kExpertGroup; ++g) {
-      const int e = min(e0 + g, E - 1);
-      const uint4* w4 = reinterpret_cast<const uint4*>(wr + static_cast<size_t>(e) * H);
-#pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        int c = lane + SF_WAVE * i;
-        wv[g][i] = c < nchunks ? w4[c] : make_uint4(0, 0, 0, 0);
-      }
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + SF_WAVE * i;
+      hreg[tt][i] = c < nchunks ? h4[c] : make_uint4(0, 0, 0, 0);
     }
-    float acc[kExpertGroup];
+  }
 #pragma unroll
-    for (int g = 0; g < kExpertGroup; ++g) {
-      acc[g] = 0.0f;
+  for (int g = 0; g < EPW; ++g) {
+    const uint4* w4 = reinterpret_cast<const uint4*>(wr + static_cast<size_t>(min(e0 + g, E - 1)) * H);
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = lane + SF_WAVE * i;
+      wv[g][i] = c < nchunks ? w4[c] : make_uint4(0, 0, 0, 0);
+    }
+  }
+  float acc[TT][EPW];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int g = 0; g < EPW; ++g) {
+      acc[tt][g] = 0.0f;
 #pragma unroll
       for (int i = 0; i < NCH; ++i)
-        if (lane + SF_WAVE * i < nchunks) acc[g] = dot8_acc(hreg[i], wv[g][i], acc[g]);
+        if (lane + SF_WAVE * i < nchunks) acc[tt][g] = dot8_acc(hreg[tt][i], wv[g][i], acc[tt][g]);
     }
+  // Lane tt*EPW + g stores logit (t0+tt, e0+g).
+  float a = 0.0f;
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
+  for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-      for (int g = 0; g < kExpertGroup; ++g) acc[g] += __shfl_xor(acc[g], d, SF_WAVE);
+    for (int g = 0; g < EPW; ++g) {
+      const float total = sf_wave_sum(acc[tt][g]);
+      if (lane == tt * EPW + g) a = total;
     }
-    if (lane < kExpertGroup && e0 + lane < E) {
-      float a = acc[0];
-#pragma unroll
-      for (int g = 1; g < kExpertGroup; ++g)
-        if (lane == g) a = acc[g];
-      const uint16_t b = sf_f32_to_bf16(a);
-      logits[static_cast<size_t>(t) * E + e0 + lane] = b;
-      s_logit[e0 + lane] = sf_bf16_to_f32(b);
-    }
-  }
-  __syncthreads();
-  if (wave == 0)
-    softmax_topk_wave(s_logit, E, K, renorm, topw + static_cast<size_t>(t) * K,
-                      topi + static_cast<size_t>(t) * K, s_val, s_id);
+  const int t = t0 + lane / EPW;
+  const int e = e0 + lane % EPW;
+  if (lane < TT * EPW && t < T && e < E)
+    logits[static_cast<size_t>(t) * E + e] = sf_f32_to_bf16(a);
+}
+
+constexpr int kSelectWaves = 4;
+
+__global__ __launch_bounds__(kSelectWaves * SF_WAVE) void router_select_kernel(
+    const uint16_t* __restrict__ logits, int T, int E, int K, int renorm,
+    uint16_t* __restrict__ topw, int64_t* __restrict__ topi) {
+  __shared__ float s_logit[kSelectWaves][SF_MAX_EXPERTS];
+  __shared__ float s_val[kSelectWaves][SF_MAX_TOPK];
+  __shared__ int s_id[kSelectWaves][SF_MAX_TOPK];
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+  const int wave = threadIdx.x / SF_WAVE;
+  const int t = blockIdx.x * kSelectWaves + wave;
+  if (t >= T) return;  // wave-uniform; the kernel has no block barrier
+  // Lane l writes and later reads only experts l, l+64, ...: no barrier.
+  for (int e = lane; e < E; e += SF_WAVE)
+    s_logit[wave][e] = sf_bf16_to_f32(logits[static_cast<size_t>(t) * E + e]);
+  softmax_topk_wave(s_logit[wave], E, K, renorm, topw + static_cast<size_t>(t) * K,
+                    topi + static_cast<size_t>(t) * K, s_val[wave], s_id[wave]);
 }
 
 // Scalar path for any hidden_size / alignment: same summation order.
@@ -224,7 +223,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_scalar_kernel(
         if (k < H) acc = __builtin_fmaf(sf_bf16_to_f32(h[k]), sf_bf16_to_f32(w[k]), acc);
       }
     }
-    acc = wave_sum_butterfly(acc);
+    acc = sf_wave_sum(acc);
     if (lane == 0) {
       uint16_t b = sf_f32_to_bf16(acc);
       logits[static_cast<size_t>(t) * E + e] = b;
@@ -261,21 +260,32 @@ extern "C" int sf_router_topk(const void* hidden, const void* router_weight,
                        (hidden_size % 8 == 0);
   const int nchunks = (hidden_size + 7) / 8;
   const int per_lane = (nchunks + SF_WAVE - 1) / SF_WAVE;
-  dim3 grid(tokens), block(kRouterThreads);
   if (aligned && per_lane <= 16) {
-    block = dim3(kRouterVecThreads);
+    int tt = 1, epw = 1;
+    auto logits_launch = [&](auto kernel, int tile_tokens, int tile_experts) {
+      tt = tile_tokens;
+      epw = tile_experts;
+      const int per_block = kLogitWaves * epw;
+      dim3 grid((tokens + tt - 1) / tt, (num_experts + per_block - 1) / per_block);
+      kernel<<<grid, dim3(kLogitWaves * SF_WAVE), 0, s>>>(h, w, tokens, hidden_size, num_experts, lg);
+    };
     if (per_lane <= 1)
-      router_topk_vec_kernel<1><<<grid, block, 0, s>>>(h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
+      logits_launch(router_logits_kernel<1>, LogitTile<1>::tokens, LogitTile<1>::experts);
     else if (per_lane <= 2)
-      router_topk_vec_kernel<2><<<grid, block, 0, s>>>(h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
+      logits_launch(router_logits_kernel<2>, LogitTile<2>::tokens, LogitTile<2>::experts);
     else if (per_lane <= 4)
-      router_topk_vec_kernel<4><<<grid, block, 0, s>>>(h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
+      logits_launch(router_logits_kernel<4>, LogitTile<4>::tokens, LogitTile<4>::experts);
     else if (per_lane <= 8)
-      router_topk_vec_kernel<8><<<grid, block, 0, s>>>(h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
+      logits_launch(router_logits_kernel<8>, LogitTile<8>::tokens, LogitTile<8>::experts);
     else
-      router_topk_vec_kernel<16><<<grid, block, 0, s>>>(h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
+      logits_launch(router_logits_kernel<16>, LogitTile<16>::tokens, LogitTile<16>::experts);
+    SF_LAUNCH_CHECK();
+    router_select_kernel<<<dim3((tokens + kSelectWaves - 1) / kSelectWaves),
+                           dim3(kSelectWaves * SF_WAVE), 0, s>>>(lg, tokens, num_experts, top_k,
+                                                                 norm_topk_prob, tw, topk_index);
   } else {
-    router_topk_scalar_kernel<<<grid, block, 0, s>>>(h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
+    router_topk_scalar_kernel<<<dim3(tokens), dim3(kRouterThreads), 0, s>>>(
+        h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
   }
   SF_LAUNCH_CHECK();
   return SF_OK;

@@ -57,6 +57,41 @@ __device__ __forceinline__ float sf_silu(float x) {
   return x / (1.0f + __expf(-x));
 }
 
+// Value of x in the lane that DPP control CTRL selects (a register move
+// across lanes, no LDS).
+template <int CTRL>
+__device__ __forceinline__ float sf_dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float sf_readlane(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Sum of the 64 lanes' x by the xor butterfly over distances 1, 2, 4, 8,
+// 16, 32 (v[l] += v[l ^ d]), bit for bit, returned wave-uniform.  IEEE
+// addition is commutative, so after distance d every aligned group of 2d
+// lanes holds one value; the half-row and row mirrors (lane i <-> 7-i,
+// i <-> 15-i) then deliver the same value as lane i ^ 4 and i ^ 8, and the
+// four rows (r0..r3) finish as (r0 + r1) + (r2 + r3).
+__device__ __forceinline__ float sf_wave_sum(float x) {
+  x += sf_dpp<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+  x += sf_dpp<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  x += sf_dpp<0x141>(x);  // row_half_mirror
+  x += sf_dpp<0x140>(x);  // row_mirror
+  return (sf_readlane(x, 0) + sf_readlane(x, 16)) + (sf_readlane(x, 32) + sf_readlane(x, 48));
+}
+
+// Maximum of the 64 lanes' x (fmaxf; exact in any order), wave-uniform.
+__device__ __forceinline__ float sf_wave_max(float x) {
+  x = fmaxf(x, sf_dpp<0xB1>(x));
+  x = fmaxf(x, sf_dpp<0x4E>(x));
+  x = fmaxf(x, sf_dpp<0x141>(x));
+  x = fmaxf(x, sf_dpp<0x140>(x));
+  return fmaxf(fmaxf(sf_readlane(x, 0), sf_readlane(x, 16)),
+               fmaxf(sf_readlane(x, 32), sf_readlane(x, 48)));
+}
+
 #define SF_HIP_CHECK(expr)                                        \
   do {                                                            \
     hipError_t sf_err__ = (expr);                                 \
