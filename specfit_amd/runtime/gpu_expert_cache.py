@@ -22,6 +22,7 @@ an SDMA transfer that leaves the compute units to the expert GEMMs).
 """
 from __future__ import annotations
 
+import itertools
 from collections import deque
 from dataclasses import dataclass, field, replace
 from threading import RLock
@@ -55,6 +56,7 @@ class _Slot:
     last_used_sequence: int = 0
     ready_event: torch.cuda.Event | None = None
     use_events: dict = field(default_factory=dict)
+    write_stream: torch.cuda.Stream | None = None  # stream of the last H2D into the slot
 
     def lru_key(self) -> tuple:
         return (self.expert_id is not None, self.last_used_sequence, self.slot_id)
@@ -85,6 +87,10 @@ class _ExpertCacheCheckpoint:
     sequence: int
     submission_sequence: int
     state_version: int
+
+
+_shared_stream_cache_ids = itertools.count()
+_READER_POLL_NS = 50_000_000  # host wait for a slot's reader before an H2D (see _await_reader)
 
 
 class _Pin:
@@ -119,7 +125,14 @@ class GpuExpertCache:
                  device: torch.device | str, adopt_pinned_sources: bool = False,
                  cache_id: str | None = None, queue_id: str | None = None,
                  observer: CacheTransitionObserver | None = None,
-                 source_owner: _SourceOwner | None = None) -> None:
+                 source_owner: _SourceOwner | None = None,
+                 copy_streams: tuple[torch.cuda.Stream, torch.cuda.Stream] | None = None) -> None:
+        """``copy_streams``: the two SDMA streams the cache's transfers
+        alternate between, instead of a pair of its own.  The layer caches
+        of one model share a pair: layers copy one after another, and one
+        pair keeps the transfers on the same two engine queues (per-cache
+        pairs of 48 layers ran at ~89% of the link rate that one pair
+        reaches)."""
         if not cpu_sources:
             raise ValueError("cpu_sources must contain at least one expert")
         if slot_count <= 0:
@@ -161,20 +174,30 @@ class GpuExpertCache:
             self._source_order[expert_id] = order
             self._canonical_keys[expert_id] = expert_id
 
+        if copy_streams is not None:
+            if (len(copy_streams) != 2 or copy_streams[0] is copy_streams[1]
+                    or any(not isinstance(st, torch.cuda.Stream) or st.device != self.device
+                           for st in copy_streams)):
+                raise ValueError("copy_streams must be two distinct streams of the cache device")
         with torch.cuda.device(self.device):
-            self.copy_stream = torch.cuda.Stream(device=self.device)
             # A second SDMA stream: consecutive transfers alternate between the
             # two so one engine's per-transfer setup overlaps the other's data
             # movement (9 MiB copies reach ~98% of the host-link peak instead
             # of ~92% on one stream).  Used only while copy_stream is the
-            # cache's own stream.
+            # cache's first stream.
+            if copy_streams is None:
+                self.copy_stream = torch.cuda.Stream(device=self.device)
+                self._aux_copy_stream = torch.cuda.Stream(device=self.device)
+            else:
+                self.copy_stream, self._aux_copy_stream = copy_streams
             self._own_copy_stream = self.copy_stream
-            self._aux_copy_stream = torch.cuda.Stream(device=self.device)
             storage = torch.empty((slot_count, *shape), dtype=dtype, device=self.device)
             # The allocation may be recycled memory whose earlier readers are
             # still queued on the current stream: order the first copy after them.
             self.copy_stream.wait_stream(torch.cuda.current_stream(self.device))
             self._aux_copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+        if cache_id is None and copy_streams is not None:
+            cache_id = f"cuda-{self.device.index}-cache-{next(_shared_stream_cache_ids)}"
         self.cache_id = cache_id or f"cuda-{self.device.index}-stream-{int(self.copy_stream.cuda_stream)}"
         self.queue_id = queue_id or f"{self.cache_id}-copy"
         self._storage = storage
@@ -392,6 +415,7 @@ class GpuExpertCache:
                 s.active_leases = 0
                 s.last_used_sequence = 0
                 s.ready_event = None
+                s.write_stream = None
                 s.use_events.clear()
             self._stats = _Counters()
             self._sequence = 0
@@ -435,7 +459,8 @@ class GpuExpertCache:
             copied = perf_counter_ns()
             torch.cuda.current_stream(self.device).synchronize()
             synced = perf_counter_ns()
-            self._slots = [replace(s, tensor=self._storage[s.slot_id], use_events=dict(s.use_events))
+            self._slots = [replace(s, tensor=self._storage[s.slot_id], use_events=dict(s.use_events),
+                                   write_stream=None)
                            for s in checkpoint.slots]
             self._resident = dict(checkpoint.resident)
             self._table_version += 1
@@ -539,16 +564,18 @@ class GpuExpertCache:
         guards = tuple(slot.use_events.values())
         slot.use_events.clear()
         stream = self._transfer_stream()
-        if slot.ready_event is not None:
+        if slot.ready_event is not None and slot.write_stream is not stream:
             # Writes of one slot stay in submission order even when the
-            # previous one ran on the other stream.
+            # previous one ran on the other stream (on the same stream the
+            # stream order already keeps them).
             stream.wait_event(slot.ready_event)
         for guard in guards:
-            stream.wait_event(guard)
+            self._await_reader(stream, guard)
         ops.copy_h2d(slot.tensor, self._sources[expert_id], stream)
         ready = torch.cuda.Event(blocking=False)
         ready.record(stream)
         slot.ready_event = ready
+        slot.write_stream = stream
         transfer = _Transfer(expert_id, slot.slot_id, slot.generation,
                              self._submission_sequence, ready)
         self._inflight[expert_id] = transfer
@@ -562,6 +589,23 @@ class GpuExpertCache:
             self._record_transition(kind=RuntimeEventKind.H2D_SUBMIT, expert_id=expert_id,
                                     slot=slot, submission_sequence=transfer.submission_sequence,
                                     ready_event=ready)
+
+    @staticmethod
+    def _await_reader(stream: torch.cuda.Stream, guard: torch.cuda.Event) -> None:
+        """Order a slot's next H2D after a kernel that read the slot.  The
+        host waits for the reader (polling, at most _READER_POLL_S) rather
+        than the copy stream: a copy stream that waits on compute-stream
+        events while compute kernels wait on its own ready events stalls
+        between copies on MI355X (9 MiB copies fell from 57 to 32-50 GB/s in
+        that pattern, and back to 57 with the waits on the host).  A reader
+        still running after the poll window gets the device-side wait."""
+        if guard.query():
+            return
+        deadline = perf_counter_ns() + _READER_POLL_NS
+        while perf_counter_ns() < deadline:
+            if guard.query():
+                return
+        stream.wait_event(guard)
 
     def _transfer_stream(self) -> torch.cuda.Stream:
         """Stream of the next H2D: alternate the cache's two SDMA streams by

@@ -218,13 +218,16 @@ def _install(model, *, layer_packed: dict[int, torch.Tensor], device: torch.devi
              h2d_prefetch: bool, cache_observer) -> tuple:
     config = model.config
     caches = []
+    # One pair of SDMA streams for every layer cache (layers copy in turn).
+    copy_streams = (torch.cuda.Stream(device=device), torch.cuda.Stream(device=device))
     try:
         for layer_id, layer in enumerate(model.model.layers):
             packed = layer_packed[layer_id]
             cache = GpuExpertCache({ExpertKey(layer_id, e): packed[e] for e in range(packed.shape[0])},
                                    slot_count=slots_per_layer, device=device,
                                    adopt_pinned_sources=True, cache_id=f"qwen3-layer-{layer_id}",
-                                   queue_id=f"layer-{layer_id}-copy", observer=cache_observer)
+                                   queue_id=f"layer-{layer_id}-copy", observer=cache_observer,
+                                   copy_streams=copy_streams)
             caches.append(cache)
             layer.mlp.experts = Qwen3OffloadedExperts(
                 layer_id=layer_id, cache=cache, hidden_size=config.hidden_size,
