@@ -217,12 +217,15 @@ class Qwen3OffloadedExperts(nn.Module):
         cache = self.cache
         dev = hidden_states.device
         with cache._lock:
+            # Host work before K2, so the table launch follows the counts
+            # read without a host gap.
             version, slots, pending = cache._slot_table(self._keys)
             table = self._upload_slot_table(version, slots, dev)
+            routes = self._new_routes(hidden_states, top_k_weights, None)
+            stream = torch.cuda.current_stream(dev)
             plan = _dispatch(top_k_index, num_experts)
             plan.start_counts(self._counts_staging(num_experts))
-            routes = self._new_routes(hidden_states, top_k_weights, plan)
-            stream = torch.cuda.current_stream(dev)
+            routes.plan = plan
             for ready in pending:  # transfers still in flight
                 stream.wait_event(ready)
             entry = ops.grouped_swiglu_table(routes.hidden, plan, routes.route_weights, table,
@@ -335,7 +338,7 @@ class Qwen3OffloadedExperts(nn.Module):
         return counts
 
     def _new_routes(self, hidden_states, top_k_weights, plan) -> _GroupedRoutes:
-        T, K = plan.tokens, plan.top_k
+        T, K = top_k_weights.shape
         dev = hidden_states.device
         routes = _GroupedRoutes(
             hidden=hidden_states.contiguous(),

@@ -367,10 +367,11 @@ def test_batched_resident_runs_keep_the_reference_lease_sequence(device):
 def test_slot_table_forward_matches_the_launch_path(device, shape):
     """After a forward that copied nothing in, a resident-first layer runs
     its resident experts from the device slot table.  Output bits, cache
-    slots, LRU and submission sequences and counters must equal those of
-    the per-launch path (the same order passed explicitly), also when the
-    table forward misses and when a token repeats an expert (an expert with
-    more rows than tokens)."""
+    slots, LRU and submission sequences, counters and (tiny shape, with
+    observers) the recorded cache transitions must equal those of the
+    per-launch path (the same order passed explicitly), also when the table
+    forward misses and when a token repeats an expert (an expert with more
+    rows than tokens)."""
     if shape == "tiny":
         E, H, I, K, slots = 12, 32, 16, 3, 10
     else:
@@ -379,14 +380,24 @@ def test_slot_table_forward_matches_the_launch_path(device, shape):
     sources = {e: (torch.randn(3 * I * H, generator=g) * 0.02).to(torch.bfloat16)
                for e in range(E)}
 
-    def stack():
+    observers = {}
+
+    def stack(name):
+        observers[name] = RecordingCacheTransitionObserver(run_id=name) if shape == "tiny" else None
         cache = GpuExpertCache({ExpertKey(0, e): t for e, t in sources.items()},
-                               slot_count=slots, device=device)
+                               slot_count=slots, device=device, cache_id="layer-0",
+                               queue_id="layer-0-copy", observer=observers[name])
         return cache, Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H,
                                             intermediate_size=I,
                                             execution_policy="resident_first", h2d_prefetch=True)
 
-    (ca, la), (cb, lb) = stack(), stack()
+    (ca, la), (cb, lb) = stack("table"), stack("launch")
+
+    def events(name):  # the cache transitions, without stream ids and timings
+        if observers[name] is None:
+            return ()
+        return tuple((e.kind, e.expert_id, e.slot_id, e.generation, e.submission_sequence,
+                      e.victim_expert_id) for e in observers[name].events())
 
     def state(cache):
         snap = cache.snapshot()
@@ -442,6 +453,9 @@ def test_slot_table_forward_matches_the_launch_path(device, shape):
         assert (len(table_calls) > calls) == uses_table
         assert torch.equal(ya, yb), step
         assert state(ca) == state(cb), step
+        assert events("table") == events("launch"), step
     assert len(table_calls) == 4  # hits only (twice), repeated expert, a miss
+    if shape == "tiny":  # the tiny stacks record their cache transitions
+        assert len(events("table")) > 100
     ca.close()
     cb.close()
