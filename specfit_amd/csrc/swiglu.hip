@@ -9,9 +9,10 @@
 // element is used m times and the GEMMs are bound by streaming the 9 MiB of
 // expert weights from HBM.  Every weight byte is read from HBM once.
 //
-// Weight stream.  A workgroup owns a slab of 32 weight rows (phase 1: the
-// 16 gate + 16 up rows of 16 activation columns; phase 2: 32 rows of D, i.e.
-// 32 output columns) and streams it in blocks of 256 k.  A block is loaded
+// Weight stream.  A workgroup owns a slab of 32 weight rows in a wide launch
+// (phase 1: the 16 gate + 16 up rows of 16 activation columns; phase 2: 32
+// rows of D, i.e. 32 output columns) or 16 in a narrow one (8 + 8 rows of 8
+// columns; 16 rows of D), and streams it in blocks of 256 k.  A block is loaded
 // row-contiguously (2 rows x 512 B per wavefront instruction, ~6.2 TB/s on
 // MI355X, where loading MFMA B fragments directly touches 16 rows x 64 B per
 // instruction and streams at ~4.4 TB/s), two blocks ahead into registers,
@@ -46,8 +47,6 @@ namespace {
 constexpr int kMaxListExperts = 128;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / SF_WAVE;
-constexpr int kGateCols = 16;          // activation columns per phase-1 workgroup
-constexpr int kDownCols = 32;          // output columns per phase-2 workgroup
 constexpr int kBlockK = 256;           // k per staged weight block
 constexpr int kRowBytes = kBlockK * 2 + 16;  // padded LDS row (bytes)
 
@@ -135,25 +134,23 @@ constexpr int kDepth = 2;             // blocks in flight ahead of the one in us
 // so loads stay in issue order and registers hold only blocks in flight.
 #define SF_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// A weight slab: rows 16g .. 16g+15 start at group[g] and are `stride`
-// elements apart.
+// A weight slab of 16*NT rows in 8-row blocks: rows 8i .. 8i+7 start at
+// part[i] and are `stride` elements apart.
 template <int NT>
 struct Slab {
-  const uint16_t* group[NT];
+  const uint16_t* part[2 * NT];
   int64_t stride;
 };
 
-// Lane l of wavefront w loads 16 B of slab rows 8i + 2w + l/32 (i < 2*NT) at
+// Lane l of wavefront w loads 16 B of slab row 8i + 2w + l/32 (i < 2*NT) at
 // k 8*(l%32) of block b.
 template <int NT>
 __device__ __forceinline__ void load_w(const Slab<NT>& w, int b, int lane, int wave,
                                        uint4 (&r)[2 * NT]) {
   const int col = b * kBlockK + (lane & 31) * 8;
+  const int64_t row = 2 * wave + (lane >> 5);
 #pragma unroll
-  for (int i = 0; i < 2 * NT; ++i) {
-    const int row = 8 * (i & 1) + 2 * wave + (lane >> 5);
-    r[i] = ld16(w.group[i >> 1] + static_cast<int64_t>(row) * w.stride + col);
-  }
+  for (int i = 0; i < 2 * NT; ++i) r[i] = ld16(w.part[i] + row * w.stride + col);
 }
 
 template <int NT>
@@ -299,30 +296,42 @@ __device__ __forceinline__ bool a_rows(RowPtr row_of, int mp, const uint16_t* (&
 }
 
 // ---------------------------------------------------------------- phase 1 --
-// Workgroup: 16 activation columns c0.. of one expert = gate rows c0.. and up
-// rows I + c0.. of GU (NT = 2).
-template <Resolve R, int MTW, int KS, int NB>
+// Workgroup: 8*NT activation columns c0.. of one expert = gate rows c0.. and
+// up rows I + c0.. of GU.  NT = 2: the gate and the up rows fill one 16-wide
+// MFMA tile each.  NT = 1: one tile holds 8 gate rows then 8 up rows, and
+// lane j < 8 of a row takes the up value from lane j + 8 (a DPP row shift).
+template <Resolve R, int MTW, int KS, int NB, int NT>
 __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWork& wk, int tile,
                                             char* smem) {
   constexpr int TM = kWaves / KS;
   constexpr int kPass = 16 * TM * MTW;
+  constexpr int kCols = 8 * NT;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int H = a.H;
-  const int c0 = tile * kGateCols;
-  Slab<2> w;
-  w.group[0] = wk.w + static_cast<int64_t>(c0) * H;
-  w.group[1] = wk.w + static_cast<int64_t>(a.I + c0) * H;
+  const int c0 = tile * kCols;
+  const uint16_t* g = wk.w + static_cast<int64_t>(c0) * H;
+  const uint16_t* u = wk.w + static_cast<int64_t>(a.I + c0) * H;
+  Slab<NT> w;
+  if constexpr (NT == 2) {
+    w.part[0] = g;
+    w.part[1] = g + static_cast<int64_t>(8) * H;
+    w.part[2] = u;
+    w.part[3] = u + static_cast<int64_t>(8) * H;
+  } else {
+    w.part[0] = g;
+    w.part[1] = u;
+  }
   w.stride = H;
   for (int p0 = 0; p0 < wk.m; p0 += kPass) {
     const int mp = min(kPass, wk.m - p0);
     const uint16_t* xr[MTW];
     const bool active = a_rows<MTW, TM>(
         [&](int row) { return row_ptr<R>(a, wk.r0 + p0 + row); }, mp, xr);
-    sf_f32x4 acc[MTW][2];
-    stream_gemm<2, MTW, KS, NB>(w, xr, wave / TM, active, smem, acc);
+    sf_f32x4 acc[MTW][NT];
+    stream_gemm<NT, MTW, KS, NB>(w, xr, wave / TM, active, smem, acc);
     bool owner = true;
-    if constexpr (KS > 1) owner = reduce_slices<2, KS>(acc, smem);
+    if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
     if (!owner) continue;
     // D layout: lane holds rows 4*(lane/16)+i, column lane%16.
 #pragma unroll
@@ -330,9 +339,17 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = (mt * TM + wave % TM) * 16 + 4 * (lane >> 4) + i;
-        if (row < mp) {
-          const float gb = sf_round_bf16(acc[mt][0][i]);
-          const float ub = sf_round_bf16(acc[mt][1][i]);
+        float gv, uv;
+        if constexpr (NT == 2) {
+          gv = acc[mt][0][i];
+          uv = acc[mt][1][i];
+        } else {
+          gv = acc[mt][0][i];
+          uv = sf_dpp<0x108>(gv);  // row_shl 8: lane j <- lane j + 8
+        }
+        if (row < mp && (NT == 2 || (lane & 15) < 8)) {
+          const float gb = sf_round_bf16(gv);
+          const float ub = sf_round_bf16(uv);
           const float sb = sf_round_bf16(sf_silu(gb));
           a.act[static_cast<int64_t>(wk.r0 + p0 + row) * a.I + c0 + (lane & 15)] =
               sf_f32_to_bf16(sb * ub);
@@ -345,40 +362,39 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
 // Row class MC of a build: 0: every expert of the launch has m <= 16, 1:
 // <= 32, 2: <= 64, 3: any.  An expert above its launch's class (max_rows
 // understated) runs in passes of the class's largest split.
-template <Resolve R, int MC, int NB>
+template <Resolve R, int MC, int NB, int NT>
 __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const SwigluArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * 32 * kRowBytes];
-  const int tiles = a.I / kGateCols;
+  __shared__ __attribute__((aligned(16))) char smem[2 * 16 * NT * kRowBytes];
+  const int tiles = a.I / (8 * NT);
   const int j = blockIdx.x / tiles;
   const int tile = blockIdx.x - j * tiles;
   ExpertWork wk;
   if (!resolve<R>(a, j, wk)) return;
   if (MC == 0 || wk.m <= 16)
-    gateup_body<R, 1, 4, NB>(a, wk, tile, smem);
+    gateup_body<R, 1, 4, NB, NT>(a, wk, tile, smem);
   else if (MC == 1 || wk.m <= 32)
-    gateup_body<R, 1, 2, NB>(a, wk, tile, smem);
+    gateup_body<R, 1, 2, NB, NT>(a, wk, tile, smem);
   else if (MC == 3 && wk.m > 64)
-    gateup_body<R, 2, 1, NB>(a, wk, tile, smem);
+    gateup_body<R, 2, 1, NB, NT>(a, wk, tile, smem);
   else
-    gateup_body<R, 1, 1, NB>(a, wk, tile, smem);
+    gateup_body<R, 1, 1, NB, NT>(a, wk, tile, smem);
 }
 
 // ---------------------------------------------------------------- phase 2 --
-// Workgroup: kDownCols output columns n0.. of one expert over the full I.
-template <Resolve R, int MTW, int KS, int NB>
+// Workgroup: 16*NT output columns n0.. of one expert over the full I.
+template <Resolve R, int MTW, int KS, int NB, int NT>
 __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork& wk, int tile,
                                           char* smem) {
-  constexpr int NT = kDownCols / 16;
   constexpr int TM = kWaves / KS;
   constexpr int kPass = 16 * TM * MTW;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int I = a.I;
-  const int n0 = tile * kDownCols;
+  const int n0 = tile * 16 * NT;
   Slab<NT> w;
   const uint16_t* wd = wk.w + 2 * static_cast<int64_t>(a.I) * a.H + static_cast<int64_t>(n0) * I;
 #pragma unroll
-  for (int g = 0; g < NT; ++g) w.group[g] = wd + static_cast<int64_t>(16 * g) * I;
+  for (int h = 0; h < 2 * NT; ++h) w.part[h] = wd + static_cast<int64_t>(8 * h) * I;
   w.stride = I;
   for (int p0 = 0; p0 < wk.m; p0 += kPass) {
     const int mp = min(kPass, wk.m - p0);
@@ -410,22 +426,22 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
   }
 }
 
-template <Resolve R, int MC, int NB>
+template <Resolve R, int MC, int NB, int NT>
 __global__ __launch_bounds__(kThreads) void down_mfma_kernel(const SwigluArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kDownCols * kRowBytes];
-  const int tiles = a.H / kDownCols;
+  __shared__ __attribute__((aligned(16))) char smem[2 * 16 * NT * kRowBytes];
+  const int tiles = a.H / (16 * NT);
   const int j = blockIdx.x / tiles;
   const int tile = blockIdx.x - j * tiles;
   ExpertWork wk;
   if (!resolve<R>(a, j, wk)) return;
   if (MC == 0 || wk.m <= 16)
-    down_body<R, 1, 4, NB>(a, wk, tile, smem);
+    down_body<R, 1, 4, NB, NT>(a, wk, tile, smem);
   else if (MC == 1 || wk.m <= 32)
-    down_body<R, 1, 2, NB>(a, wk, tile, smem);
+    down_body<R, 1, 2, NB, NT>(a, wk, tile, smem);
   else if (MC == 3 && wk.m > 64)
-    down_body<R, 2, 1, NB>(a, wk, tile, smem);
+    down_body<R, 2, 1, NB, NT>(a, wk, tile, smem);
   else
-    down_body<R, 1, 1, NB>(a, wk, tile, smem);
+    down_body<R, 1, 1, NB, NT>(a, wk, tile, smem);
 }
 
 // ------------------------------------------------ generic (any shape) path --
@@ -487,14 +503,41 @@ bool mfma_shape_ok(int H, int I) {
   return H == kNbGateup * kBlockK && I == kNbDown * kBlockK;
 }
 
-template <Resolve R, int MC>
-int launch_mfma(const SwigluArgs& a, long long g1, long long g2, hipStream_t s) {
-  gateup_mfma_kernel<R, MC, kNbGateup>
+template <Resolve R, int MC, int NT>
+int launch_mfma(const SwigluArgs& a, int groups, hipStream_t s) {
+  const long long g1 = static_cast<long long>(groups) * (a.I / (8 * NT));
+  const long long g2 = static_cast<long long>(groups) * (a.H / (16 * NT));
+  if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
+  gateup_mfma_kernel<R, MC, kNbGateup, NT>
       <<<dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
-  down_mfma_kernel<R, MC, kNbDown><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
+  down_mfma_kernel<R, MC, kNbDown, NT><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
   return SF_OK;
+}
+
+// Tile width.  A narrow launch (8 activation columns per gate/up workgroup,
+// 16 output columns per down workgroup) has twice the workgroups of a wide
+// one (16 / 32), so a launch of few small experts covers more CUs; each of
+// its workgroups re-reads the expert's token rows, so the narrow form costs
+// more than it gains once a launch carries many experts or experts of more
+// than 16 rows.  Measured on MI355X at the Qwen3-30B-A3B shape: 1-4 experts
+// of <= 16 rows run 10-15% faster narrow, ~120 experts of <= 16 rows 2%
+// slower, 12 experts of <= 64 rows no faster when their weights were just
+// copied in.  Both widths give bit-identical results: a column's summation
+// order does not depend on the tile it sits in.
+constexpr int kNarrowMaxGroups = 24;
+
+bool narrow_tiles(int groups, int max_rows) {
+  return max_rows <= 16 && groups <= kNarrowMaxGroups;
+}
+
+template <Resolve R, int NT>
+int launch_class(const SwigluArgs& a, int groups, int max_rows, hipStream_t s) {
+  if (max_rows <= 16) return launch_mfma<R, 0, NT>(a, groups, s);
+  if (max_rows <= 32) return launch_mfma<R, 1, NT>(a, groups, s);
+  if (max_rows <= 64) return launch_mfma<R, 2, NT>(a, groups, s);
+  return launch_mfma<R, 3, NT>(a, groups, s);
 }
 
 // max_rows bounds the rows of any expert of the launch; it picks the row
@@ -503,13 +546,8 @@ template <Resolve R>
 int launch(const SwigluArgs& a, int groups, bool mfma, int max_rows, hipStream_t s) {
   if (groups <= 0) return SF_OK;
   if (mfma) {
-    const long long g1 = static_cast<long long>(groups) * (a.I / kGateCols);
-    const long long g2 = static_cast<long long>(groups) * (a.H / kDownCols);
-    if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
-    if (max_rows <= 16) return launch_mfma<R, 0>(a, g1, g2, s);
-    if (max_rows <= 32) return launch_mfma<R, 1>(a, g1, g2, s);
-    if (max_rows <= 64) return launch_mfma<R, 2>(a, g1, g2, s);
-    return launch_mfma<R, 3>(a, g1, g2, s);
+    if (narrow_tiles(groups, max_rows)) return launch_class<R, 1>(a, groups, max_rows, s);
+    return launch_class<R, 2>(a, groups, max_rows, s);
   }
   gateup_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();

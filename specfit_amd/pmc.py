@@ -22,13 +22,14 @@ import argparse
 import csv
 import glob
 import os
+import re
 import sys
 from collections import defaultdict
 
 CALIBRATION_BYTES = 256 << 20   # read and written by the calibration kernel
 CALIBRATION_TAG = "neg"         # substring of the calibration kernel's name
 HIDDEN, INTERMEDIATE = 2048, 768
-GATEUP_COLS, DOWN_COLS, THREADS = 16, 32, 256
+THREADS = 256
 
 
 def _rows(run_dir: str) -> list[dict]:
@@ -55,11 +56,22 @@ def _per_dispatch(run_dir: str, counter: str) -> list[tuple[int, str, int, float
     return [(d, *acc[d]) for d in sorted(acc)]
 
 
+def _tile_width(name: str) -> int:
+    """The kernel's last template argument: 1 for narrow tiles (8 gate/up
+    columns, 16 down columns per workgroup), 2 for wide ones (16 / 32)."""
+    m = re.search(r"_mfma_kernel<([^<>]*)>", name)
+    if not m:
+        raise ValueError(f"no template arguments in kernel name {name!r}")
+    return int(m.group(1).split(",")[-1])
+
+
 def _k3_weight_bytes(name: str, grid: int) -> int | None:
     if "gateup_mfma_kernel" in name:
-        return grid // (INTERMEDIATE // GATEUP_COLS * THREADS) * 2 * INTERMEDIATE * HIDDEN * 2
+        cols = 8 * _tile_width(name)
+        return grid // (INTERMEDIATE // cols * THREADS) * 2 * INTERMEDIATE * HIDDEN * 2
     if "down_mfma_kernel" in name:
-        return grid // (HIDDEN // DOWN_COLS * THREADS) * HIDDEN * INTERMEDIATE * 2
+        cols = 16 * _tile_width(name)
+        return grid // (HIDDEN // cols * THREADS) * HIDDEN * INTERMEDIATE * 2
     return None
 
 

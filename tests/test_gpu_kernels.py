@@ -207,7 +207,10 @@ def test_grouped_swiglu_row_classes_streams_and_table(device):
     """Calls whose largest expert falls in each row class (<= 16 / 32 / 64 /
     more rows), thirty calls in a row, calls running concurrently on two
     streams and the slot-table form all give the rows of one-expert calls,
-    bit for bit."""
+    bit for bit.  One-expert calls of <= 16 rows run narrow tiles (8 gate/up,
+    16 down columns per workgroup); the all-expert calls (more than 24
+    experts) run wide ones (16 / 32), so this also pins that the two widths
+    agree bit for bit."""
     E, T, K, H, I = 32, 128, 8, 2048, 768
     layer = make_layer(seed=11, num_experts=E, zipf_s=1.1)
     hidden = make_hidden(T, seed=12, zipf_fold=True)
@@ -219,6 +222,8 @@ def test_grouped_swiglu_row_classes_streams_and_table(device):
     act = torch.empty((T * K, I), dtype=torch.bfloat16, device=device)
     ref = torch.zeros_like(rows_all)
     active = [e for e in range(E) if ms[e]]
+    assert len(active) > 24  # the all-expert calls take the wide tiles
+    assert sum(0 < m <= 16 for m in ms) >= 2  # some one-expert calls take the narrow ones
     for e in active:
         ops.grouped_swiglu(h_dev, plan, wflat, [e], [slots[e]], H, I, act, ref)
     torch.cuda.synchronize()
