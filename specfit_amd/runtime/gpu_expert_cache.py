@@ -27,7 +27,7 @@ from collections import deque
 from dataclasses import dataclass, field, replace
 from threading import RLock
 from time import perf_counter_ns
-from typing import Hashable, Mapping, Protocol
+from typing import Hashable, Mapping, Protocol, Sequence
 
 import torch
 
@@ -93,20 +93,21 @@ _shared_stream_cache_ids = itertools.count()
 _READER_POLL_NS = 50_000_000  # host wait for a slot's reader before an H2D (see _await_reader)
 
 
-class _Pin:
-    """What is left of a resident-run lease after its release bookkeeping:
-    the slot stays pinned (``active_leases``) until the kernels that read it
-    are enqueued; ``_unpin`` (or the cache's ``_unpin_many``) then records
-    the use guard and drops the pin."""
+class _PinRun:
+    """What is left of the leases of a run of resident experts after their
+    release bookkeeping (``_resident_run_unobserved``): each slot stays
+    pinned (``active_leases``) until the kernels that read it are enqueued;
+    the cache's ``_unpin_many`` (or ``_unpin``) then records the use guards
+    and drops the pins of the whole run."""
 
-    __slots__ = ("_cache", "expert_id", "slot_id", "generation", "_streams", "_unpin_pending")
+    __slots__ = ("_cache", "keys", "slot_ids", "generations", "_streams", "_unpin_pending")
 
-    def __init__(self, cache: "GpuExpertCache", expert_id: Hashable, slot_id: int,
-                 generation: int, streams: dict) -> None:
+    def __init__(self, cache: "GpuExpertCache", keys: Sequence[Hashable], slot_ids: list[int],
+                 generations: list[int], streams: dict) -> None:
         self._cache = cache
-        self.expert_id = expert_id
-        self.slot_id = slot_id
-        self.generation = generation
+        self.keys = keys
+        self.slot_ids = slot_ids
+        self.generations = generations
         self._streams = streams
         self._unpin_pending = True
 
@@ -114,8 +115,7 @@ class _Pin:
         if not self._unpin_pending:
             return
         self._unpin_pending = False
-        self._cache._unpin(self.expert_id, self.slot_id, self.generation,
-                           tuple(self._streams.values()))
+        self._cache._unpin_run(self, tuple(self._streams.values()))
 
 
 class GpuExpertCache:
@@ -155,6 +155,9 @@ class GpuExpertCache:
         # maps store these objects, so lookups with them match by identity.
         self._canonical_keys: dict[Hashable, Hashable] = {}
         self._table_version = 0  # bumped on every slot assignment, reset and restore
+        # (keys, table version, table) of the last _slot_table without
+        # transfers in flight; callers only read the table.
+        self._slot_table_cache: tuple | None = None
         self._source_order: dict[Hashable, int] = {}
         for order, (expert_id, src) in enumerate(items):
             if src.device.type != "cpu":
@@ -264,8 +267,12 @@ class GpuExpertCache:
         lock."""
         with self._lock:
             self._reap_completed_transfers()
-            resident = self._resident
             inflight = self._inflight
+            cached = self._slot_table_cache
+            if (not inflight and cached is not None and cached[0] is keys
+                    and cached[1] == self._table_version):
+                return cached[1], cached[2], []
+            resident = self._resident
             table = []
             pending = []
             for k in keys:
@@ -278,6 +285,8 @@ class GpuExpertCache:
                     else:
                         slot = -1
                 table.append(slot)
+            if not pending:  # reused while the version stands and nothing is in flight
+                self._slot_table_cache = (keys, self._table_version, table)
             return self._table_version, table, pending
 
     def is_available(self, expert_id: Hashable) -> bool:
@@ -701,6 +710,23 @@ class GpuExpertCache:
             self._record_use_guards(slot, used_streams)
             slot.active_leases -= 1
 
+    def _unpin_run(self, run: _PinRun, used_streams: tuple) -> None:
+        """``_unpin`` of every slot of a resident run: one use event per
+        stream guards the run's slots."""
+        with self._lock:
+            guards = []
+            for stream in used_streams:
+                ev = torch.cuda.Event(blocking=False)
+                ev.record(stream)
+                guards.append((int(stream.cuda_stream), ev))
+            slots = self._slots
+            for key, slot_id, generation in zip(run.keys, run.slot_ids, run.generations):
+                slot = slots[slot_id]
+                self._validate_lease(slot, key, generation)
+                for sid, ev in guards:
+                    slot.use_events[sid] = ev
+                slot.active_leases -= 1
+
     def _resident_steps(self, keys, index: int, current, stream, limit: int):
         """Run steps ``index`` .. of the layer's one-ahead lease sequence in
         one locked pass while both the step's expert and the next one are
@@ -779,102 +805,104 @@ class GpuExpertCache:
 
     def _resident_run_unobserved(self, keys, index: int, current, stream, sid: int,
                                  limit: int):
-        """``_resident_steps`` without an observer (lock held): the same
-        slot pins, LRU sequence numbers, state versions and hit counts,
-        kept in locals and written back once; the released entries are
-        ``_Pin`` records and only the lease carried out of the run is an
-        ``ExpertLease``."""
+        """``_resident_steps`` without an observer (lock held).  Step j of the
+        run (keys[index + j] and the next key both resident) does, per the
+        per-expert sequence: acquire (first step, when no lease is carried
+        in: pin + LRU touch), one-ahead prefetch of the next key (pin, hit,
+        touch deferred to its wait), the wait's deferred touch (every step
+        but a first one whose carried lease has no deferred touch), release
+        (LRU touch, slot stays pinned).  Every slot of the run is distinct,
+        so each step's slot ends with its release touch's sequence number;
+        the counters take the totals.  The released entries share one
+        ``_PinRun``; only the lease carried out of the run is an
+        ``ExpertLease``.  Everything that allocates runs before the first
+        change to the cache."""
         resident = self._resident
+        ids = [resident.get(k) for k in keys[index:index + limit + 1]]
+        if None in ids:
+            del ids[ids.index(None):]
+        steps = len(ids) - 1
+        if steps <= 0:
+            return [], index, current
         slots = self._slots
-        streams = {sid: stream}
+        run = [slots[i] for i in ids]
+        end = index + steps
+        last = run[steps]
+        ahead = ExpertLease(self, keys[end], last.slot_id, last.generation, last.ready_event,
+                            _defer_touch=True)
+        ahead._ready_known = True
+        first = 0 if current is None else 1
         out = []
-        n = len(keys)
-        seq = self._sequence
-        ver = self._state_version
-        hits = 0
-        ahead = None  # (key, slot) prefetched by the previous step, touch deferred
-        try:
-            while index + 1 < n and len(out) < limit:
-                key, nxt = keys[index], keys[index + 1]
-                slot_id, next_id = resident.get(key), resident.get(nxt)
-                if slot_id is None or next_id is None:
-                    break
-                slot = slots[slot_id]
-                carried = None
-                if ahead is not None:
-                    deferred = True
-                elif current is not None:
-                    carried, current = current, None
-                    deferred = carried._touch_on_wait
-                else:  # acquire: immediate touch
-                    hits += 1
-                    slot.active_leases += 1
-                    seq += 1
-                    ver += 1
-                    slot.last_used_sequence = seq
-                    deferred = False
-                # one-ahead prefetch of the next expert: deferred touch
-                nslot = slots[next_id]
-                hits += 1
-                nslot.active_leases += 1
-                ver += 1
-                ahead = (nxt, nslot)
-                if deferred:  # the wait's touch
-                    seq += 1
-                    ver += 1
-                    slot.last_used_sequence = seq
-                # release, keeping the slot pinned until its launch
-                seq += 1
-                ver += 1
-                slot.last_used_sequence = seq
-                if carried is not None:
-                    carried._streams[sid] = stream
-                    carried._touch_on_wait = False
-                    carried._released = True
-                    carried._unpin_pending = True
-                    pin = carried
-                else:
-                    pin = _Pin(self, key, slot_id, slot.generation, streams)
-                out.append((key.expert_id, pin, slot.tensor))
-                index += 1
-        except BaseException:
-            self._sequence, self._state_version = seq, ver
-            self._stats.resident_hits += hits
-            for _, pin, _ in out:
-                pin._unpin()
-            if ahead is not None:
-                nxt, nslot = ahead
-                ExpertLease(self, nxt, nslot.slot_id, nslot.generation, nslot.ready_event,
-                            _defer_touch=True).release()
-            raise
+        if current is not None:  # the lease carried in holds keys[index]
+            out.append((keys[index].expert_id, current, run[0].tensor))
+        if first < steps:
+            run_keys = keys[index + first:end]
+            pins = _PinRun(self, run_keys, ids[first:steps],
+                           [slot.generation for slot in run[first:steps]], {sid: stream})
+            out.extend([(k.expert_id, pins, slot.tensor)
+                        for k, slot in zip(run_keys, run[first:steps])])
+        fresh = current is None
+        if fresh:
+            deferred = False
+            run[0].active_leases += 1
+        else:
+            deferred = current._touch_on_wait
+            current._streams[sid] = stream
+            current._touch_on_wait = False
+            current._released = True
+            current._unpin_pending = True
+        seq = self._sequence + fresh + deferred
+        for j in range(steps):
+            if j:
+                seq += 1  # the wait's deferred touch
+            seq += 1      # the release touch
+            run[j].last_used_sequence = seq
+            run[j + 1].active_leases += 1
         self._sequence = seq
-        self._state_version = ver
-        self._stats.resident_hits += hits
-        if ahead is not None:
-            nxt, nslot = ahead
-            current = ExpertLease(self, nxt, nslot.slot_id, nslot.generation, nslot.ready_event,
-                                  _defer_touch=True)
-            current._ready_known = True
-        return out, index, current
+        self._state_version += fresh + 2 * steps + (steps - 1 + deferred)
+        self._stats.resident_hits += fresh + steps
+        return out, end, ahead
 
     def _unpin_many(self, leases) -> None:
-        """``_unpin`` of leases whose weights one launch read: a single use
-        event per stream, recorded after that launch, guards every slot of
-        the batch (it completes no earlier than per-lease events would)."""
+        """``_unpin`` of leases (and resident runs) whose weights one launch
+        read: a single use event per stream, recorded after that launch,
+        guards every slot of the batch (it completes no earlier than
+        per-lease events would).  A run listed once per expert is unpinned
+        once."""
         with self._lock:
             events: dict[int, torch.cuda.Event] = {}
-            for lease in leases:
-                if not lease._unpin_pending:
-                    continue
-                lease._unpin_pending = False
-                slot = self._slots[lease.slot_id]
-                self._validate_lease(slot, lease.expert_id, lease.generation)
-                for sid, stream in lease._streams.items():
+            slots = self._slots
+
+            def guards_of(streams: dict) -> list:
+                out = []
+                for sid, stream in streams.items():
                     ev = events.get(sid)
                     if ev is None:
                         ev = torch.cuda.Event(blocking=False)
                         ev.record(stream)
                         events[sid] = ev
+                    out.append((sid, ev))
+                return out
+
+            for lease in leases:
+                if not lease._unpin_pending:
+                    continue
+                lease._unpin_pending = False
+                guards = guards_of(lease._streams)
+                if lease.__class__ is _PinRun:
+                    for key, slot_id, generation in zip(lease.keys, lease.slot_ids,
+                                                        lease.generations):
+                        slot = slots[slot_id]
+                        if ((slot.expert_id is not key and slot.expert_id != key)
+                                or slot.generation != generation or slot.active_leases <= 0):
+                            raise RuntimeError("expert lease refers to a reused GPU slot")
+                        for sid, ev in guards:
+                            slot.use_events[sid] = ev
+                        slot.active_leases -= 1
+                    continue
+                slot = slots[lease.slot_id]
+                self._validate_lease(slot, lease.expert_id, lease.generation)
+                for sid, ev in guards:
                     slot.use_events[sid] = ev
                 slot.active_leases -= 1
 

@@ -37,6 +37,7 @@ from __future__ import annotations
 from contextlib import closing
 from dataclasses import dataclass
 from enum import Enum
+from itertools import compress
 from typing import Sequence
 
 import torch
@@ -233,7 +234,7 @@ class Qwen3OffloadedExperts(nn.Module):
                                              self.intermediate_size, routes.act, routes.rows,
                                              max_rows=T, tag="resident")
             counts = self._read_counts(plan, top_k_index, num_experts)
-            active = tuple(e for e in range(num_experts) if counts[e])
+            active = tuple(compress(range(num_experts), counts))
             routes.covered = frozenset(e for e in active if slots[e] >= 0 and counts[e] <= T)
             if entry is not None:
                 entry[0] = len(routes.covered)
@@ -320,7 +321,7 @@ class Qwen3OffloadedExperts(nn.Module):
         num_experts = self.num_experts()
         plan = _dispatch(top_k_index, num_experts)
         counts = self._read_counts(plan, top_k_index, num_experts)
-        active = tuple(e for e in range(num_experts) if counts[e])
+        active = tuple(compress(range(num_experts), counts))
         return self._new_routes(hidden_states, top_k_weights, plan), active
 
     def _counts_staging(self, num_experts: int) -> torch.Tensor:
@@ -505,8 +506,12 @@ class Qwen3OffloadedExperts(nn.Module):
             return order
         if self.execution_policy is ExpertExecutionPolicy.EXPERT_ID_ASCENDING:
             return active_experts
-        resident = self.cache._resident_key_set()
+        cache = self.cache
         keys = self._keys
-        hits = tuple(e for e in active_experts if keys[e] in resident)
-        misses = tuple(e for e in active_experts if keys[e] not in resident)
-        return hits + misses
+        hits, misses = [], []
+        with cache._lock:
+            cache._reap_completed_transfers()
+            resident = cache._resident
+            for e in active_experts:
+                (hits if keys[e] in resident else misses).append(e)
+        return tuple(hits + misses)
