@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 5
+#define SF_ABI_VERSION 6
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -104,11 +104,19 @@ int sf_router_topk(const void *hidden, const void *router_weight, int tokens,
  *              ascending position order (stable)
  *   inv_perm   int32 [tokens * top_k]   permuted row of each route position
  *              (-1 for an out-of-range entry)
+ *   host_meta  NULL, or pinned host memory (hipHostMalloc) of int32
+ *              [2, num_experts + 1]: the kernel also writes counts (row 0)
+ *              and offsets (row 1) there, so the caller reads the routes per
+ *              expert once the stream passes the kernel, with no separate
+ *              device-to-host copy (the reference's one host read of the
+ *              routed experts, qwen3_offloaded_experts.py:111-113).  Memory
+ *              the device cannot map returns SF_ERR_INVALID_ARGUMENT.
  * One workgroup; any tokens >= 0.
  */
 int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
                 int num_experts, int32_t *counts, int32_t *offsets,
-                int32_t *perm_pos, int32_t *inv_perm, sf_stream_t stream);
+                int32_t *perm_pos, int32_t *inv_perm, int32_t *host_meta,
+                sf_stream_t stream);
 
 /*
  * K3: grouped SwiGLU expert MLP over dispatched rows.  Replaces the per-expert

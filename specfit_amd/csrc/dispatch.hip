@@ -20,7 +20,7 @@ constexpr int kDispatchWaves = kDispatchThreads / SF_WAVE;
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const int64_t* __restrict__ idx, int N, int E, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm_pos,
-    int32_t* __restrict__ inv_perm) {
+    int32_t* __restrict__ inv_perm, int32_t* __restrict__ host_meta) {
   __shared__ int s_total[SF_MAX_EXPERTS];
   __shared__ int s_offset[SF_MAX_EXPERTS + 1];
   __shared__ int s_running[SF_MAX_EXPERTS];
@@ -85,6 +85,16 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     counts[E] = s_invalid;
     offsets[E] = s_offset[E];
   }
+  if (host_meta) {  // the same [counts; offsets] into pinned host memory
+    for (int e = tid; e < E; e += kDispatchThreads) {
+      host_meta[e] = s_total[e];
+      host_meta[E + 1 + e] = s_offset[e];
+    }
+    if (tid == 0) {
+      host_meta[E] = s_invalid;
+      host_meta[2 * E + 1] = s_offset[E];
+    }
+  }
 
   // Pass 2: stable scatter, chunk by chunk.
   const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (SF_WAVE - lane));
@@ -140,7 +150,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
 
 extern "C" int sf_dispatch(const int64_t* topk_index, int tokens, int top_k,
                            int num_experts, int32_t* counts, int32_t* offsets,
-                           int32_t* perm_pos, int32_t* inv_perm,
+                           int32_t* perm_pos, int32_t* inv_perm, int32_t* host_meta,
                            sf_stream_t stream) {
   if (tokens < 0 || top_k < 1 || num_experts < 1 || num_experts > SF_MAX_EXPERTS)
     return SF_ERR_INVALID_ARGUMENT;
@@ -148,9 +158,16 @@ extern "C" int sf_dispatch(const int64_t* topk_index, int tokens, int top_k,
   if (n > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
   if (!counts || !offsets) return SF_ERR_INVALID_ARGUMENT;
   if (n > 0 && (!topk_index || !perm_pos || !inv_perm)) return SF_ERR_INVALID_ARGUMENT;
+  int32_t* host_dev = nullptr;  // the device's address of host_meta
+  if (host_meta) {
+    void* p = nullptr;
+    if (hipHostGetDevicePointer(&p, host_meta, 0) != hipSuccess || !p)
+      return SF_ERR_INVALID_ARGUMENT;
+    host_dev = static_cast<int32_t*>(p);
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dispatch_kernel<<<1, kDispatchThreads, 0, s>>>(topk_index, static_cast<int>(n), num_experts,
-                                                 counts, offsets, perm_pos, inv_perm);
+                                                 counts, offsets, perm_pos, inv_perm, host_dev);
   SF_LAUNCH_CHECK();
   return SF_OK;
 }

@@ -281,25 +281,44 @@ class DispatchPlan:
 
 
 def dispatch(index: torch.Tensor, num_experts: int, *,
-             stream: torch.cuda.Stream | None = None) -> DispatchPlan:
-    """Stable counting sort of the [T,K] routes by expert id (K2)."""
+             stream: torch.cuda.Stream | None = None,
+             host_meta: torch.Tensor | None = None) -> DispatchPlan:
+    """Stable counting sort of the [T,K] routes by expert id (K2).
+
+    ``host_meta``: a pinned int32 [2, num_experts + 1] buffer that the
+    kernel also writes [counts; offsets] into; the plan's counts read then
+    waits for the kernel instead of enqueuing a copy.  The caller keeps the
+    buffer untouched until it has read the counts (``fetch_counts``)."""
     _require_cuda("top_k_index", index, torch.int64)
     if index.ndim != 2:
         raise ValueError("top_k_index must have shape [tokens, top_k]")
+    shape = (2, num_experts + 1)
+    if host_meta is not None and (host_meta.shape != shape or host_meta.dtype != torch.int32
+                                  or not host_meta.is_pinned() or not host_meta.is_contiguous()):
+        raise ValueError("host_meta must be pinned contiguous int32 [2, num_experts + 1]")
     index = index.contiguous()
     T, K = index.shape
     dev = index.device
-    meta = torch.empty((2, num_experts + 1), dtype=torch.int32, device=dev)
+    meta = torch.empty(shape, dtype=torch.int32, device=dev)
     perm = torch.empty(T * K, dtype=torch.int32, device=dev)
     inv = torch.empty(T * K, dtype=torch.int32, device=dev)
+    plan = DispatchPlan(T, K, int(num_experts), meta, perm, inv)
     if T * K == 0:
         meta.zero_()
-        return DispatchPlan(T, K, int(num_experts), meta, perm, inv)
+        if host_meta is not None:
+            host_meta.zero_()
+            plan.host_counts = host_meta
+            plan.count_list = host_meta[0].tolist()
+        return plan
+    handle = _stream_handle(stream, dev)
     rc = _native.lib().sf_dispatch(_ptr(index), T, K, int(num_experts), _ptr(meta[0]),
-                                   _ptr(meta[1]), _ptr(perm), _ptr(inv),
-                                   _stream_handle(stream, dev))
+                                   _ptr(meta[1]), _ptr(perm), _ptr(inv), _ptr(host_meta), handle)
     _native.check(rc, "sf_dispatch")
-    return DispatchPlan(T, K, int(num_experts), meta, perm, inv)
+    if host_meta is not None:
+        ev = torch.cuda.Event()
+        ev.record(stream if stream is not None else torch.cuda.current_stream(dev))
+        plan._counts_event = (ev, host_meta)
+    return plan
 
 
 # ------------------------------------------------------------------ K3 ----

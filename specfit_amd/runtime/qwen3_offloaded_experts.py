@@ -8,9 +8,10 @@ the same constructor, ``forward`` signature and ValueErrors, and the
 One layer forward:
 
 1. K2 ``sf_dispatch`` stably sorts the T*K routes by expert id on the device
-   (replaces torch.sort / unique_consecutive / where, :111-122, :173-178); the
-   host reads the [E+1] counts once (the layer's only device-to-host sync --
-   the reference has the same one) to know the active experts.
+   (replaces torch.sort / unique_consecutive / where, :111-122, :173-178) and
+   also writes the [E+1] counts into the layer's pinned staging buffer; the
+   host waits for K2 and reads them once (the layer's only device-to-host
+   sync -- the reference has the same one) to know the active experts.
 2. Experts are leased from the ``GpuExpertCache`` in the reference's order
    and with its acquire / one-ahead prefetch / release sequence
    (:205-230), so LRU state, generations, statistics and observer events
@@ -80,9 +81,11 @@ class _GroupedRoutes:
     covered: frozenset = frozenset()  # experts whose rows a slot-table launch computed
 
 
-def _dispatch(top_k_index: torch.Tensor, num_experts: int) -> ops.DispatchPlan:
-    """Seam: K2 dispatch of one layer's routes."""
-    return ops.dispatch(top_k_index, num_experts)
+def _dispatch(top_k_index: torch.Tensor, num_experts: int,
+              host_meta: torch.Tensor | None = None) -> ops.DispatchPlan:
+    """Seam: K2 dispatch of one layer's routes (with ``host_meta``, the
+    kernel also writes the counts the layer reads into that pinned buffer)."""
+    return ops.dispatch(top_k_index, num_experts, host_meta=host_meta)
 
 
 def _expert_forward(hidden_states: torch.Tensor, packed_weights, *, hidden_size: int,
@@ -224,8 +227,7 @@ class Qwen3OffloadedExperts(nn.Module):
             table = self._upload_slot_table(version, slots, dev)
             routes = self._new_routes(hidden_states, top_k_weights, None)
             stream = torch.cuda.current_stream(dev)
-            plan = _dispatch(top_k_index, num_experts)
-            plan.start_counts(self._counts_staging(num_experts))
+            plan = _dispatch(top_k_index, num_experts, self._counts_staging(num_experts))
             routes.plan = plan
             for ready in pending:  # transfers still in flight
                 stream.wait_event(ready)
@@ -319,7 +321,7 @@ class Qwen3OffloadedExperts(nn.Module):
         if T == 0 or K == 0:
             return None, ()
         num_experts = self.num_experts()
-        plan = _dispatch(top_k_index, num_experts)
+        plan = _dispatch(top_k_index, num_experts, self._counts_staging(num_experts))
         counts = self._read_counts(plan, top_k_index, num_experts)
         active = tuple(compress(range(num_experts), counts))
         return self._new_routes(hidden_states, top_k_weights, plan), active

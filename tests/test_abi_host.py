@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_error_strings():
-    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 5
+    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 6
     assert _native.error_string(0) == "success"
     assert _native.error_string(1) == "invalid argument"
     assert _native.error_string(12345) != ""
@@ -53,7 +53,7 @@ def test_host_side_validation_needs_no_device():
     assert lib.sf_router_topk(null, null, 4, 32, 4, 5, 1, null, null, null, null) == 1
     assert lib.sf_router_topk(null, null, -1, 32, 4, 2, 1, null, null, null, null) == 1
     assert lib.sf_router_topk(null, null, 0, 32, 4, 2, 1, null, null, null, null) == 0
-    assert lib.sf_dispatch(null, 4, 8, 300, null, null, null, null, null) == 1
+    assert lib.sf_dispatch(null, 4, 8, 300, null, null, null, null, null, null) == 1
     assert lib.sf_combine(null, null, null, null, 4, 64, 128, 2048, 0, null, null) == 1
     assert lib.sf_grouped_swiglu(null, null, null, null, 4, 8, 2048, 768, -1, 1, null, null, null,
                                  null, null) == 1

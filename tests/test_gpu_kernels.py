@@ -41,7 +41,7 @@ def _router_case(device, T, H, E, K, renorm, seed, hidden=None, weight=None):
     np.testing.assert_array_equal(_bits(tw), o_w)
 
 
-@pytest.mark.parametrize("T,seed", [(16, 0), (64, 1), (1, 2), (128, 3)])
+@pytest.mark.parametrize("T,seed", [(16, 0), (64, 1), (1, 2), (128, 3), (300, 5)])
 def test_router_bitexact_qwen3_shape(device, T, seed):
     _router_case(device, T, 2048, 128, 8, True, seed)
 
@@ -87,6 +87,15 @@ def _dispatch_case(device, idx: np.ndarray, E: int):
     valid = int(offsets[E])
     np.testing.assert_array_equal(plan.perm_pos.cpu().numpy()[:valid], perm[:valid])
     np.testing.assert_array_equal(plan.inv_perm.cpu().numpy(), inv)
+    # The kernel's own write of [counts; offsets] into pinned host memory
+    # (read after waiting for the kernel only) and the copied read agree.
+    host = torch.full((2, E + 1), -7, dtype=torch.int32, pin_memory=True)
+    plan2 = ops.dispatch(t, E, host_meta=host)
+    got = plan2.fetch_counts().numpy()
+    np.testing.assert_array_equal(got[0], counts)
+    np.testing.assert_array_equal(got[1], offsets)
+    assert plan2.count_list == counts.tolist()
+    np.testing.assert_array_equal(plan.fetch_counts().numpy(), got)
 
 
 @pytest.mark.parametrize("T,K,E,seed", [(64, 8, 128, 0), (1, 8, 128, 1), (16, 8, 128, 2),
@@ -111,6 +120,18 @@ def test_dispatch_duplicates_skew_and_invalid(device):
 def test_dispatch_empty(device):
     plan = ops.dispatch(torch.zeros((0, 8), dtype=torch.int64, device=device), 128)
     assert plan.fetch_counts()[0].sum().item() == 0
+    host = torch.full((2, 129), 5, dtype=torch.int32, pin_memory=True)
+    plan = ops.dispatch(torch.zeros((0, 8), dtype=torch.int64, device=device), 128, host_meta=host)
+    assert plan.fetch_counts().sum().item() == 0 and plan.count_list == [0] * 129
+
+
+def test_dispatch_rejects_unmapped_host_meta(device):
+    idx = torch.zeros((4, 8), dtype=torch.int64, device=device)
+    with pytest.raises(ValueError, match="pinned"):
+        ops.dispatch(idx, 128, host_meta=torch.zeros((2, 129), dtype=torch.int32))
+    with pytest.raises(ValueError, match="pinned"):
+        ops.dispatch(idx, 128, host_meta=torch.zeros((2, 128), dtype=torch.int32,
+                                                     pin_memory=True))
 
 
 def test_combine_bitexact_both_modes(device):
