@@ -227,20 +227,20 @@ class DispatchPlan:
         return self.meta[1]
 
     def fetch_counts(self, staging: torch.Tensor | None = None) -> torch.Tensor:
-        """Copy [counts; offsets] to pinned host memory in one transfer and
-        wait for it.  ``staging`` is a reusable pinned int32 [2, E+1] buffer;
-        without one a pinned buffer is allocated (which may synchronise the
-        device while the allocator grows, so hot paths pass one)."""
+        """[counts; offsets] in pinned host memory: waits for dispatch when it
+        wrote them there (``dispatch(..., host_meta=...)``), else copies them
+        in one transfer and waits for it.  ``staging`` is a reusable pinned
+        int32 [2, E+1] buffer for the copy; without one a pinned buffer is
+        allocated (which may synchronise the device while the allocator
+        grows, so hot paths pass one)."""
         if self.host_counts is None:
             self.start_counts(staging)
         return self.finish_counts()
 
-    def start_counts(self, staging: torch.Tensor | None = None,
-                     stream: torch.cuda.Stream | None = None) -> None:
-        """Enqueue the [counts; offsets] copy without waiting
-        (``finish_counts`` waits).  With ``stream`` the copy runs there,
-        after the dispatch enqueued so far on the current stream, so work
-        enqueued later on the current stream does not delay the read."""
+    def start_counts(self, staging: torch.Tensor | None = None) -> None:
+        """Enqueue the [counts; offsets] copy on the current stream without
+        waiting (``finish_counts`` waits).  Nothing to do when the read is
+        already started, or when dispatch wrote the counts to host memory."""
         if self.host_counts is not None or self._counts_event is not None:
             return
         shape = (2, self.num_experts + 1)
@@ -249,14 +249,8 @@ class DispatchPlan:
         elif staging.shape != shape or staging.dtype != torch.int32 or not staging.is_pinned():
             raise ValueError("staging must be pinned int32 [2, num_experts + 1]")
         ev = torch.cuda.Event()
-        if stream is None:
-            staging.copy_(self.meta, non_blocking=True)
-            ev.record(torch.cuda.current_stream(self.meta.device))
-        else:
-            stream.wait_stream(torch.cuda.current_stream(self.meta.device))
-            with torch.cuda.stream(stream):
-                staging.copy_(self.meta, non_blocking=True)
-            ev.record(stream)
+        staging.copy_(self.meta, non_blocking=True)
+        ev.record(torch.cuda.current_stream(self.meta.device))
         self._counts_event = (ev, staging)
 
     def finish_counts(self) -> torch.Tensor:
