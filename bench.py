@@ -17,7 +17,10 @@ Every workload runs two passes of --steps steps.  The timed pass carries no
 timing events: `value` and `ms_per_step` come from it.  The recorded pass,
 over the next inputs, brackets every K3 launch (and each step's copy window)
 with HIP events: the roofline, H2D, overlap and link-busy figures come from
-it (--record none skips it).
+it, and so do the per-step device times (K1 start to K4 end, H2D waits
+included; median and 10th/90th percentile in `device_ms_per_step`).
+--record none skips it.  Steps per pass default to 50 (10 for the 48-layer
+forwards).
 
 Prints ONE JSON line on stdout; diagnostics go to stderr.
 """
@@ -40,7 +43,8 @@ def log(msg: str) -> None:
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--steps", type=int, default=None,
+                   help="steps per pass (default 50; 10 for the 48-layer forwards)")
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--tokens", type=int, default=64)
     p.add_argument("--slots", type=int, default=24)
@@ -64,7 +68,20 @@ def parse_args():
     p.add_argument("--record", choices=("full", "k3", "none"), default="full",
                    help="timing events of the recorded pass: K3 launches + one copy window "
                         "per step (full), K3 only, or none (no recorded pass)")
-    return p.parse_args()
+    args = p.parse_args()
+    if args.steps is None:
+        args.steps = 10 if args.workload in ("verify48", "cold48") else 50
+    return args
+
+
+def step_stats(events) -> dict | None:
+    """Median and 10th/90th percentile of per-step device times (ms) from
+    (start, end) TimingEvent pairs recorded on the compute stream."""
+    if not events:
+        return None
+    ms = sorted(a.elapsed_time(b) for a, b in events)
+    pick = lambda q: ms[min(len(ms) - 1, int(q * (len(ms) - 1) + 0.5))]
+    return {"median": pick(0.5), "p10": pick(0.1), "p90": pick(0.9), "n": len(ms)}
 
 
 def cpu_baseline(layer, hidden_list, seconds: float) -> dict | None:
@@ -197,8 +214,12 @@ def main_verify(args) -> int:
         torch.cuda.synchronize()
         log("warm-up done")
 
+        compute = torch.cuda.current_stream(dev)
+        step_events = []
+
         def run_steps(first, recorder=None):
-            """(wall seconds, misses, hits, accepted nodes) of steps first..+steps."""
+            """(wall seconds, misses, hits, accepted nodes) of steps first..+steps;
+            with a recorder, a device-time event pair per step too."""
             wall = 0.0
             misses = hits = accepted = 0
             for i in range(first, first + args.steps):
@@ -207,9 +228,14 @@ def main_verify(args) -> int:
                 before = [c.stats() for c in loaded.expert_caches]
                 torch.cuda.synchronize()
                 start = time.perf_counter()
+                if recorder is not None:
+                    ev = (ops.TimingEvent(), ops.TimingEvent())
+                    ev[0].record(compute)
                 accepted += len(step(i).accepted_node_ids)
                 if recorder is not None:
                     recorder.close_copy_window()
+                    ev[1].record(compute)
+                    step_events.append(ev)
                 torch.cuda.synchronize()
                 wall += time.perf_counter() - start
                 after = [c.stats() for c in loaded.expert_caches]
@@ -265,6 +291,7 @@ def main_verify(args) -> int:
                      "launches": len(k3), "avg_launch_us": k3_time / max(len(k3), 1) * 1e6},
         "cpu_baseline": None,
         "recorded_ms_per_step": rec_wall / args.steps * 1e3 if rec_wall else None,
+        "device_ms_per_step": step_stats(step_events),
         "h2d": {"achieved_gbs": rec_misses * expert_bytes / h2d_time / 1e9 if h2d_time else None,
                 "transfers": rec_misses, "busy_ms": h2d_time * 1e3,
                 "link_busy_frac": h2d_time / rec_wall if h2d_time else None},
@@ -310,16 +337,25 @@ def main_sweep(args) -> int:
             _, w, idx = router(h)
             return experts(h, idx, w), idx
 
+        compute = torch.cuda.current_stream(dev)
+        step_events = []
+
         def run_steps(inputs, recorder=None):
-            """(wall seconds, misses, hits, routing indices) of one pass."""
+            """(wall seconds, misses, hits, routing indices) of one pass; with
+            a recorder, a device-time event pair per step too."""
             before = cache.stats()
             idxs = []
             torch.cuda.synchronize()
             start = time.perf_counter()
             for h in inputs:
+                if recorder is not None:
+                    ev = (ops.TimingEvent(), ops.TimingEvent())
+                    ev[0].record(compute)
                 idxs.append(step(h)[1])
                 if recorder is not None:
                     recorder.close_copy_window()
+                    ev[1].record(compute)
+                    step_events.append(ev)
             torch.cuda.synchronize()
             wall = time.perf_counter() - start
             after = cache.stats()
@@ -350,6 +386,7 @@ def main_sweep(args) -> int:
             "tokens": T, "tokens_per_s": args.steps * T / wall,
             "ms_per_step": wall / args.steps * 1e3,
             "recorded_ms_per_step": rec_wall / args.steps * 1e3 if rec_wall else None,
+            "device_ms_per_step": step_stats(step_events),
             "misses_per_step": misses / args.steps,
             "hits_per_step": hits / args.steps,
             "distinct_experts_per_step": len(ms) / args.steps,
@@ -442,15 +479,25 @@ def main() -> int:
         step(hidden[args.prewarm + i])
     torch.cuda.synchronize()
 
+    compute = torch.cuda.current_stream(dev)
+    step_events = []
+
     def run_steps(inputs, recorder=None):
-        """(wall seconds, misses, hits) of one pass over ``inputs``."""
+        """(wall seconds, misses, hits) of one pass over ``inputs``; with a
+        recorder, also a device-time event pair per step (K1 start .. K4
+        end, H2D waits included) into ``step_events``."""
         before = cache.stats()
         torch.cuda.synchronize()
         start = time.perf_counter()
         for h in inputs:
+            if recorder is not None:
+                ev = (ops.TimingEvent(), ops.TimingEvent())
+                ev[0].record(compute)
             step(h)
             if recorder is not None:
                 recorder.close_copy_window()
+                ev[1].record(compute)
+                step_events.append(ev)
         torch.cuda.synchronize()
         wall = time.perf_counter() - start
         after = cache.stats()
@@ -584,6 +631,7 @@ def main() -> int:
                    "execution_policy": "resident_first", "h2d_prefetch": True},
         "record": args.record,
         "recorded_ms_per_step": rec_wall / args.steps * 1e3 if rec_wall else None,
+        "device_ms_per_step": step_stats(step_events),
         "roofline": {"bound": "hbm", "achieved": k3_achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": k3_achieved / HBM_PEAK_GBS,
                      "traffic": ratio * k3_weight_per_launch if ratio and k3 else None,
