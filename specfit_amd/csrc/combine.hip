@@ -30,7 +30,8 @@ __device__ __forceinline__ void unpack8(uint4 q, uint16_t* v) {
 }
 
 // One block per (token, 2048-column slice).  Threads 0..K-1 fetch the
-// token's routes in parallel; thread 0 orders them in LDS.  Up to
+// token's routes in parallel and each places its route at its rank in
+// (key, position) order (the routes ordered before it, counted in LDS).  Up to
 // kPrefetch rows are then loaded before any addition so the gather costs one
 // memory round trip, and the additions run in the fixed order.
 constexpr int kPrefetch = 8;
@@ -54,23 +55,21 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
     s_rowid[j] = ok ? r : -1;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    // Insertion sort on (rank, position); equal keys keep position order.
-    int key[SF_MAX_TOPK];
-    int n = 0;
-    for (int j = 0; j < K; ++j) {
-      if (s_rowid[j] < 0) continue;
-      const int k = s_key[j];
-      int p = n++;
-      while (p > 0 && key[p - 1] > k) {
-        key[p] = key[p - 1];
-        s_row[p] = s_row[p - 1];
-        --p;
-      }
-      key[p] = k;
-      s_row[p] = s_rowid[j];
+  if (threadIdx.x < K) {
+    // Stable order on (key, position): a route's slot is the number of
+    // valid routes with a smaller key, or an equal key at an earlier position.
+    const int j = threadIdx.x;
+    const int row = s_rowid[j];
+    const int k = s_key[j];
+    int pos = 0, n = 0;
+    for (int i = 0; i < K; ++i) {
+      if (s_rowid[i] < 0) continue;
+      ++n;
+      const int ki = s_key[i];
+      pos += (ki < k) || (ki == k && i < j);
     }
-    s_n = n;
+    if (row >= 0) s_row[pos] = row;
+    if (j == 0) s_n = n;
   }
   __syncthreads();
   const int c0 = blockIdx.y * kColsPerBlock + threadIdx.x * kColsPerThread;

@@ -39,9 +39,12 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
   if (tid == 0) s_invalid = 0;
   __syncthreads();
 
-  // Pass 1: histogram (integer atomics are order independent).
+  // Pass 1: histogram (integer atomics are order independent).  Each
+  // thread keeps its first id (position tid) for the first scatter chunk.
+  int64_t first = -1;
   for (int i = tid; i < N; i += kDispatchThreads) {
     int64_t e = idx[i];
+    if (i == tid) first = e;
     if (e >= 0 && e < E)
       atomicAdd(&s_total[e], 1);
     else
@@ -102,7 +105,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const int i = base + tid;
     int e = -1;
     if (i < N) {
-      int64_t v = idx[i];
+      const int64_t v = base == 0 ? first : idx[i];
       e = (v >= 0 && v < E) ? static_cast<int>(v) : -1;
     }
     const bool valid = e >= 0;
@@ -138,6 +141,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
         inv_perm[i] = -1;
       }
     }
+    if (base + kDispatchThreads >= N) break;  // last chunk: nothing to reset
     __syncthreads();
     // Reset the per-wavefront table for the next chunk.
     for (int j = tid; j < kDispatchWaves * SF_MAX_EXPERTS; j += kDispatchThreads)

@@ -46,10 +46,10 @@ __device__ __forceinline__ float dot8_acc(uint4 hv, uint4 wv, float acc) {
 // reads only experts l, l+64, ... of s_logit.  Each top-k round takes the
 // wave maximum of the unselected probabilities and the lowest expert id
 // holding it (ballots per 64-expert slice, lowest lane first).
+template <int J>  // experts per lane: E <= 64 * J
 __device__ void softmax_topk_wave(const float* s_logit, int E, int K, int renorm,
                                   uint16_t* topw, int64_t* topi, float* s_val,
                                   int* s_id) {
-  constexpr int J = SF_MAX_EXPERTS / SF_WAVE;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   float m = -__builtin_inff();
 #pragma unroll
@@ -184,6 +184,7 @@ __global__ __launch_bounds__(kLogitWaves * SF_WAVE) void router_logits_kernel(
 
 constexpr int kSelectWaves = 4;
 
+template <int J>  // experts per lane: E <= 64 * J
 __global__ __launch_bounds__(kSelectWaves * SF_WAVE) void router_select_kernel(
     const uint16_t* __restrict__ logits, int T, int E, int K, int renorm,
     uint16_t* __restrict__ topw, int64_t* __restrict__ topi) {
@@ -197,8 +198,8 @@ __global__ __launch_bounds__(kSelectWaves * SF_WAVE) void router_select_kernel(
   // Lane l writes and later reads only experts l, l+64, ...: no barrier.
   for (int e = lane; e < E; e += SF_WAVE)
     s_logit[wave][e] = sf_bf16_to_f32(logits[static_cast<size_t>(t) * E + e]);
-  softmax_topk_wave(s_logit[wave], E, K, renorm, topw + static_cast<size_t>(t) * K,
-                    topi + static_cast<size_t>(t) * K, s_val[wave], s_id[wave]);
+  softmax_topk_wave<J>(s_logit[wave], E, K, renorm, topw + static_cast<size_t>(t) * K,
+                       topi + static_cast<size_t>(t) * K, s_val[wave], s_id[wave]);
 }
 
 // Scalar path for any hidden_size / alignment: same summation order.
@@ -232,8 +233,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_scalar_kernel(
   }
   __syncthreads();
   if (wave == 0)
-    softmax_topk_wave(s_logit, E, K, renorm, topw + static_cast<size_t>(t) * K,
-                      topi + static_cast<size_t>(t) * K, s_val, s_id);
+    softmax_topk_wave<SF_MAX_EXPERTS / SF_WAVE>(s_logit, E, K, renorm,
+                                                topw + static_cast<size_t>(t) * K,
+                                                topi + static_cast<size_t>(t) * K, s_val, s_id);
 }
 
 }  // namespace
@@ -280,9 +282,18 @@ extern "C" int sf_router_topk(const void* hidden, const void* router_weight,
     else
       logits_launch(router_logits_kernel<16>, LogitTile<16>::tokens, LogitTile<16>::experts);
     SF_LAUNCH_CHECK();
-    router_select_kernel<<<dim3((tokens + kSelectWaves - 1) / kSelectWaves),
-                           dim3(kSelectWaves * SF_WAVE), 0, s>>>(lg, tokens, num_experts, top_k,
-                                                                 norm_topk_prob, tw, topk_index);
+    // Experts per lane of the select wavefront: dead slots (e >= E) add +0
+    // to the lane sums and are never selected, so J only trims the loops.
+    const dim3 sgrid((tokens + kSelectWaves - 1) / kSelectWaves), sblock(kSelectWaves * SF_WAVE);
+    if (num_experts <= SF_WAVE)
+      router_select_kernel<1><<<sgrid, sblock, 0, s>>>(lg, tokens, num_experts, top_k,
+                                                       norm_topk_prob, tw, topk_index);
+    else if (num_experts <= 2 * SF_WAVE)
+      router_select_kernel<2><<<sgrid, sblock, 0, s>>>(lg, tokens, num_experts, top_k,
+                                                       norm_topk_prob, tw, topk_index);
+    else
+      router_select_kernel<SF_MAX_EXPERTS / SF_WAVE><<<sgrid, sblock, 0, s>>>(
+          lg, tokens, num_experts, top_k, norm_topk_prob, tw, topk_index);
   } else {
     router_topk_scalar_kernel<<<dim3(tokens), dim3(kRouterThreads), 0, s>>>(
         h, w, hidden_size, num_experts, top_k, norm_topk_prob, lg, tw, topk_index);
