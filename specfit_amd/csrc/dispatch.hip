@@ -3,8 +3,8 @@
 // unique_consecutive / route_tokens of the reference
 // (src/specfit/runtime/qwen3_offloaded_experts.py:173-178).
 //
-// One workgroup of 1024 threads walks the N = tokens*top_k route positions in
-// chunks of 1024.  Per chunk every wavefront ranks its lanes among equal
+// One workgroup walks the N = tokens*top_k route positions in chunks of its
+// thread count.  Per chunk every wavefront ranks its lanes among equal
 // expert ids with a ballot loop (rank = lanes below with the same id), the
 // per-wavefront counts are prefix-summed per expert in wavefront order, and
 // each route lands at offsets[e] + (routes of e in earlier chunks) +
@@ -14,13 +14,15 @@
 
 namespace {
 
-constexpr int kDispatchThreads = 1024;
-constexpr int kDispatchWaves = kDispatchThreads / SF_WAVE;
-
+// One workgroup of kDispatchThreads (1024, or 256 when the routes fit one
+// 256-wide chunk: fewer wavefronts to synchronise).  The permutation is the
+// unique stable order either way.
+template <int kDispatchThreads>
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const int64_t* __restrict__ idx, int N, int E, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm_pos,
     int32_t* __restrict__ inv_perm, int32_t* __restrict__ host_meta) {
+  constexpr int kDispatchWaves = kDispatchThreads / SF_WAVE;
   __shared__ int s_total[SF_MAX_EXPERTS];
   __shared__ int s_offset[SF_MAX_EXPERTS + 1];
   __shared__ int s_running[SF_MAX_EXPERTS];
@@ -120,11 +122,13 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
       pending &= ~same;
     }
     __syncthreads();
-    // Exclusive prefix over wavefronts, per expert, continuing the running
+    // Exclusive prefix over the wavefronts that hold routes in this chunk
+    // (the others' counts are zero), per expert, continuing the running
     // count of earlier chunks.
+    const int busy_waves = min(kDispatchWaves, (min(N - base, kDispatchThreads) + SF_WAVE - 1) / SF_WAVE);
     for (int ex = tid; ex < E; ex += kDispatchThreads) {
       int run = s_running[ex];
-      for (int w = 0; w < kDispatchWaves; ++w) {
+      for (int w = 0; w < busy_waves; ++w) {
         int c = s_wave_count[w][ex];
         s_wave_count[w][ex] = run;
         run += c;
@@ -170,8 +174,12 @@ extern "C" int sf_dispatch(const int64_t* topk_index, int tokens, int top_k,
     host_dev = static_cast<int32_t*>(p);
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  dispatch_kernel<<<1, kDispatchThreads, 0, s>>>(topk_index, static_cast<int>(n), num_experts,
-                                                 counts, offsets, perm_pos, inv_perm, host_dev);
+  if (n <= 256)
+    dispatch_kernel<256><<<1, 256, 0, s>>>(topk_index, static_cast<int>(n), num_experts, counts,
+                                           offsets, perm_pos, inv_perm, host_dev);
+  else
+    dispatch_kernel<1024><<<1, 1024, 0, s>>>(topk_index, static_cast<int>(n), num_experts, counts,
+                                             offsets, perm_pos, inv_perm, host_dev);
   SF_LAUNCH_CHECK();
   return SF_OK;
 }
