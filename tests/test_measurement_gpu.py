@@ -1,0 +1,39 @@
+"""bench.py's output contract on a GPU: one JSON line on stdout with the
+metric, whole-job value, roofline and CPU-baseline objects, run briefly
+(2 timed + 2 recorded steps) as a child process."""
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_bench_prints_one_contract_line(device):
+    cmd = [sys.executable, "-u", os.path.join(ROOT, "bench.py"), "--steps", "2", "--warmup", "1",
+           "--prewarm", "2", "--cpu-seconds", "0.5", "--resident-reps", "2"]
+    print("bench contract run:", " ".join(cmd[2:]), flush=True)
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=110, cwd=ROOT)
+    assert out.returncode == 0, out.stderr[-3000:]
+    lines = [line for line in out.stdout.splitlines() if line.strip()]
+    assert len(lines) == 1, out.stdout[-2000:]
+    d = json.loads(lines[0])
+    assert d["metric"].startswith("verified tree tokens/s per MoE layer")
+    assert d["unit"] == "tokens/s" and d["value"] > 0 and d["n_gpus"] == 1
+    assert d["steps"] == 2 and d["warmup"] == 1 and d["higher_is_better"] is True
+    assert d["value"] == pytest.approx(2 * 64 / (d["ms_per_step"] * 2e-3), rel=1e-6)
+    assert d["vs_baseline"] is None and d["dtype"] == "bf16" and d["data"].startswith("synthetic")
+    assert "64 tree tokens" in d["config"]["workload"]
+    r = d["roofline"]
+    assert r["bound"] == "hbm" and r["unit"] == "GB/s" and r["peak"] == 8000.0
+    assert 0 < r["achieved"] < r["peak"] and r["frac"] == pytest.approx(r["achieved"] / r["peak"])
+    assert r["traffic"] is None or r["traffic"] > 0
+    c = d["cpu_baseline"]
+    assert c["kind"] == "port" and c["value"] > 0 and c["cores"] >= 1 and c["sample"]
+    assert d["device_ms_per_step"]["n"] == 2
+    assert d["h2d"]["link_peak_gbs"] > 0 and 0 <= d["overlap"] <= 1
+

@@ -1,0 +1,157 @@
+"""CPU checks of the measurement code: the rocprofv3 summaries of
+specfit_amd/pmc.py on synthetic counter and trace files, and the bench
+helpers (copy/K3 interval union, per-step statistics, the committed traffic
+ratio, per-workload step defaults)."""
+import csv
+import os
+import subprocess
+import sys
+
+import pytest
+
+import bench
+from specfit_amd import pmc
+
+H, I = pmc.HIDDEN, pmc.INTERMEDIATE
+GATEUP_BYTES = 2 * I * H * 2     # gate + up rows of one expert
+DOWN_BYTES = H * I * 2
+
+
+def _name(kind: str, nt: int, mc: int = 2) -> str:
+    nb = 8 if kind == "gateup" else 3
+    return (f"void (anonymous namespace)::{kind}_mfma_kernel<((anonymous namespace)::Resolve)0, "
+            f"{mc}, {nb}, {nt}>((anonymous namespace)::SwigluArgs)")
+
+
+def _grid(kind: str, nt: int, experts: int) -> int:
+    tiles = I // (8 * nt) if kind == "gateup" else H // (16 * nt)
+    return experts * tiles * pmc.THREADS
+
+
+def test_tile_width_and_weight_bytes_from_kernel_names():
+    for nt in (1, 2):
+        for n in (1, 3, 45):
+            assert pmc._k3_weight_bytes(_name("gateup", nt), _grid("gateup", nt, n)) == n * GATEUP_BYTES
+            assert pmc._k3_weight_bytes(_name("down", nt), _grid("down", nt, n)) == n * DOWN_BYTES
+    assert pmc._tile_width(_name("down", 1)) == 1
+    assert pmc._k3_weight_bytes("void combine_kernel<true>(...)", 1024) is None
+    with pytest.raises(ValueError):
+        pmc._tile_width("gateup_mfma_kernel(no template)")
+
+
+CAL = "void at::native::vectorized_elementwise_kernel<4, at::native::neg_kernel_cuda(...)>"
+
+
+def _counter_dir(tmp_path, name, counter, rows):
+    d = tmp_path / name
+    d.mkdir()
+    with open(d / "k3_counter_collection.csv", "w", newline="") as fh:
+        w = csv.writer(fh)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"])
+        for i, (kname, grid, kib) in enumerate(rows):
+            # two partial rows per dispatch (the summary adds them)
+            w.writerow([i, kname, grid, counter, kib / 2])
+            w.writerow([i, kname, grid, counter, kib / 2])
+    return str(d)
+
+
+def test_traffic_summary_calibrates_and_splits_phases(tmp_path):
+    # FETCH counts half the bytes (scale 2), WRITE counts all (scale 1).
+    cal_kib = (256 << 20) / 1024
+    launches_in = [(2, 3), (1, 5)]   # (tile width, experts) of the in-step launches
+    fetch, write = [], []
+    for nt, n in launches_in:
+        for kind, wb in (("gateup", GATEUP_BYTES), ("down", DOWN_BYTES)):
+            fetch.append((_name(kind, nt), _grid(kind, nt, n), n * wb * 1.05 / 1024 / 2))
+            write.append((_name(kind, nt), _grid(kind, nt, n), n * wb * 0.01 / 1024))
+    fetch.append((CAL, 1 << 20, cal_kib / 2))
+    write.append((CAL, 1 << 20, cal_kib))
+    for kind, wb in (("gateup", GATEUP_BYTES), ("down", DOWN_BYTES)):  # all-resident, 45 experts
+        fetch.append((_name(kind, 2), _grid(kind, 2, 45), 45 * wb * 1.02 / 1024 / 2))
+        write.append((_name(kind, 2), _grid(kind, 2, 45), 0.0))
+    text = pmc.summarize(_counter_dir(tmp_path, "fetch", "FETCH_SIZE", fetch),
+                         _counter_dir(tmp_path, "write", "WRITE_SIZE", write), command="cmd")
+    ratios = {line.split(":")[0]: float(line.split(":")[1]) for line in text.splitlines()
+              if line.startswith("traffic_ratio_")}
+    assert ratios["traffic_ratio_in_step"] == pytest.approx(1.06, abs=1e-6)
+    assert ratios["traffic_ratio_all_resident"] == pytest.approx(1.02, abs=1e-6)
+    assert "| FETCH_SIZE |" in text and "2.0000" in text and "    cmd" in text
+
+
+def test_traffic_summary_rejects_mismatched_runs(tmp_path):
+    row = (_name("gateup", 2), _grid("gateup", 2, 1), 100.0)
+    other = (_name("down", 2), _grid("down", 2, 1), 100.0)
+    cal = (CAL, 1 << 20, 1000.0)
+    f = _counter_dir(tmp_path, "f", "FETCH_SIZE", [row, other, cal])
+    w = _counter_dir(tmp_path, "w", "WRITE_SIZE", [other, row, cal])
+    with pytest.raises(RuntimeError, match="different K3 dispatch sequences"):
+        pmc.summarize(f, w)
+    nocal = _counter_dir(tmp_path, "n", "FETCH_SIZE", [row, other])
+    with pytest.raises(RuntimeError, match="calibration"):
+        pmc.summarize(nocal, w)
+
+
+def test_trace_summary_averages_k3_launches_per_phase(tmp_path):
+    d = tmp_path / "trace"
+    d.mkdir()
+    rows, t = [], 0
+    def add(name, grid, dur_ns):
+        nonlocal t
+        rows.append({"Kernel_Name": name, "Grid_Size_X": grid, "Start_Timestamp": t,
+                     "End_Timestamp": t + dur_ns})
+        t += dur_ns + 1000
+    for _ in range(3):  # in-step: 2 experts, narrow, gate/up 10 us + down 6 us
+        add(_name("gateup", 1, 0), _grid("gateup", 1, 2), 10_000)
+        add(_name("down", 1, 0), _grid("down", 1, 2), 6_000)
+    add(CAL, 1 << 20, 90_000)
+    add(_name("gateup", 2), _grid("gateup", 2, 45), 55_000)
+    add(_name("down", 2), _grid("down", 2, 45), 33_000)
+    with open(d / "k3_kernel_trace.csv", "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    with open(d / "k3_kernel_stats.csv", "w", newline="") as fh:
+        w = csv.writer(fh)
+        w.writerow(["Name", "Calls", "AverageNs", "MinNs", "MaxNs", "Percentage"])
+        w.writerow([_name("gateup", 2), 1, 55000, 55000, 55000, 40.0])
+    text = pmc.summarize_trace(str(d))
+    lines = {l.split("|")[1].strip(): l for l in text.splitlines()
+             if l.startswith("| in-step") or l.startswith("| all-resident")}
+    in_step = [c.strip() for c in lines["in-step"].split("|")[1:-1]]
+    assert in_step[1:5] == ["3", "10.00", "6.00", "16.00"]
+    assert float(in_step[5]) == pytest.approx(2 * (GATEUP_BYTES + DOWN_BYTES) / 1e6, abs=0.01)
+    resident = [c.strip() for c in lines["all-resident"].split("|")[1:-1]]
+    assert resident[1:5] == ["1", "55.00", "33.00", "88.00"]
+    assert "`gateup_mfma_kernel<(Resolve)0, 2, 8, 2>`" in text
+
+
+class _Ev:
+    def __init__(self, t):
+        self.t = t
+
+    def elapsed_time(self, other):
+        return other.t - self.t
+
+
+def test_bench_helpers():
+    assert bench._union_length([(0, 2), (1, 3), (5, 6)]) == 4
+    assert bench._union_length([]) == 0
+    assert bench.step_stats([]) is None
+    st = bench.step_stats([(_Ev(0), _Ev(x)) for x in (5.0, 1.0, 3.0, 2.0, 4.0)])
+    assert st == {"median": 3.0, "p10": 1.0, "p90": 5.0, "n": 5}
+    ratio, source = bench._traffic_ratio()
+    assert 1.0 <= ratio < 1.2 and source.startswith("profiles/k3_traffic")
+
+
+@pytest.mark.parametrize("argv,steps", [([], 50), (["--workload", "verify48"], 10),
+                                        (["--workload", "cold48"], 10), (["--steps", "7"], 7)])
+def test_bench_step_defaults(monkeypatch, argv, steps):
+    monkeypatch.setattr(sys, "argv", ["bench.py", *argv])
+    assert bench.parse_args().steps == steps
+
+
+def test_bench_refuses_more_than_one_gpu():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=60, cwd=root)
+    assert out.returncode == 2 and "one GPU only" in out.stderr and not out.stdout.strip()
