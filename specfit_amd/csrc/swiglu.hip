@@ -20,7 +20,9 @@
 // keeps the fragment reads conflict-free) and read back as MFMA B fragments.
 // Token rows (the A operand, a few KiB, L2 resident) are loaded straight into
 // registers two blocks ahead, each block's right after the MFMAs that used
-// the previous contents.  The block count is a compile-time constant of the
+// the previous contents: in MFMA fragment layout, except in gate/up's split
+// for 33..64 rows, which loads them row-contiguously and passes them through
+// a per-wavefront LDS region (see mfma_block_staged).  The block count is a compile-time constant of the
 // expert shape, so the loop is unrolled and every load is unconditional: the
 // compiler's vector-memory wait counts are then exact (they are in-order
 // counters; a conditional load would force a full drain).  Scheduling
@@ -204,13 +206,62 @@ __device__ __forceinline__ void mfma_block(const char* tile, int s0, const uint4
   }
 }
 
+// Staged A operand of gate/up's one-tile, full-k split (KS = 1, one 16-row
+// tile per wavefront, experts of 33..64 rows).  Loading MFMA A fragments
+// straight from memory touches 16 token rows x 64 B per instruction; here a
+// wavefront loads its 16 rows row-contiguously instead (4 rows x 256 B per
+// instruction: half as many cache lines per byte), writes each half block to
+// its own LDS region and reads the fragments back.  The MFMA operands are the
+// same values, so the results are the same bits.
+constexpr int kStageRowBytes = (kBlockK / 2) * 2 + 16;  // half a block of one row (bytes), padded
+constexpr int kStageBytes = 16 * kStageRowBytes;      // one wavefront's region
+
+// Lane l loads 16 B at element 8*(l%16) of the half block j/4 of row
+// l/16 + 4*(j%4) of the tile (xr[i] = row l/16 + 4i, offset 8*(l%16)).
+__device__ __forceinline__ void load_x_rows(const uint16_t* const (&xr)[4], int b,
+                                            uint4 (&x)[1][kSteps]) {
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j) x[0][j] = ld16(xr[j & 3] + b * kBlockK + (j >> 2) * (kBlockK / 2));
+}
+
+template <int NT>
+__device__ __forceinline__ void mfma_block_staged(const char* tile, char* stage,
+                                                  const uint4 (&x)[1][kSteps], int lane,
+                                                  sf_f32x4 (&acc)[1][NT]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<uint4*>(stage + (4 * i + (lane >> 4)) * kStageRowBytes + (lane & 15) * 16) =
+          x[0][4 * h + i];
+    SF_SCHED_FENCE();
+#pragma unroll
+    for (int g = 0; g < 4; g += 2) {
+      uint4 a[2], f[2][NT];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        a[s] = *reinterpret_cast<const uint4*>(stage + (lane & 15) * kStageRowBytes +
+                                               (g + s) * 64 + (lane >> 4) * 16);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) f[s][nt] = frag_b(tile, 16 * nt, 4 * h + g + s, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[0][nt] = mfma16(a[s], f[s][nt], acc[0][nt]);
+    }
+  }
+}
+
 // acc = X . W^T over k-slice `slice` of KS (SP = kSteps/KS k-steps of each of
 // the NB blocks).  active: wave-uniform, false when the wavefront's tiles
 // have no rows (its A loads then hit one cache line, see a_rows).
-template <int NT, int MTW, int KS, int NB>
-__device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* const (&xr)[MTW],
-                                            int slice, bool active, char* smem,
+template <int NT, int MTW, int KS, int NB, int NP>
+__device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* const (&xr)[NP],
+                                            int slice, bool active, char* smem, char* stage,
                                             sf_f32x4 (&acc)[MTW][NT]) {
+  constexpr bool kStaged = KS == 1 && MTW == 1 && NP == 4;
   static_assert(NB >= kDepth, "fewer blocks than the prefetch depth");
   constexpr int SP = kSteps / KS;
   constexpr int kTile = 16 * NT * kRowBytes;
@@ -226,7 +277,8 @@ __device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* c
 #pragma unroll
   for (int d = 0; d < kDepth; ++d) {
     load_w<NT>(w, d, lane, wave, wr[d]);
-    load_x<MTW, SP>(xr, d, s0, xq[d]);
+    if constexpr (kStaged) load_x_rows(xr, d, xq[d]);
+    else load_x<MTW, SP>(xr, d, s0, xq[d]);
   }
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
@@ -237,9 +289,16 @@ __device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* c
     if (b + kDepth < NB) load_w<NT>(w, b + kDepth, lane, wave, wr[d]);
     SF_SCHED_FENCE();
     __syncthreads();  // tile b visible; tile b-1's reads are done
-    if (active) mfma_block<NT, MTW, SP>(tile, s0, xq[d], lane, acc);
+    if constexpr (kStaged) {
+      if (active) mfma_block_staged<NT>(tile, stage, xq[d], lane, acc);
+    } else {
+      if (active) mfma_block<NT, MTW, SP>(tile, s0, xq[d], lane, acc);
+    }
     SF_SCHED_FENCE();
-    if (b + kDepth < NB) load_x<MTW, SP>(xr, b + kDepth, s0, xq[d]);
+    if (b + kDepth < NB) {
+      if constexpr (kStaged) load_x_rows(xr, b + kDepth, xq[d]);
+      else load_x<MTW, SP>(xr, b + kDepth, s0, xq[d]);
+    }
     SF_SCHED_FENCE();
   }
   __syncthreads();  // the tiles are free again
@@ -295,6 +354,22 @@ __device__ __forceinline__ bool a_rows(RowPtr row_of, int mp, const uint16_t* (&
   return active;
 }
 
+// Row pointers of the staged split: lane l holds rows l/16 + 4i (i < 4) of
+// the wavefront's tile, clamped to the pass, at element 8*(l%16).  An idle
+// wavefront points every lane at the pass's first row.
+template <typename RowPtr>
+__device__ __forceinline__ bool a_rows_staged(RowPtr row_of, int mp, const uint16_t* (&xr)[4]) {
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+  const int wave = threadIdx.x / SF_WAVE;
+  const bool active = wave * 16 < mp;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = active ? min(wave * 16 + (lane >> 4) + 4 * i, mp - 1) : 0;
+    xr[i] = row_of(row) + 8 * (lane & 15);
+  }
+  return active;
+}
+
 // ---------------------------------------------------------------- phase 1 --
 // Workgroup: 8*NT activation columns c0.. of one expert = gate rows c0.. and
 // up rows I + c0.. of GU.  NT = 2: the gate and the up rows fill one 16-wide
@@ -325,11 +400,18 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
   w.stride = H;
   for (int p0 = 0; p0 < wk.m; p0 += kPass) {
     const int mp = min(kPass, wk.m - p0);
-    const uint16_t* xr[MTW];
-    const bool active = a_rows<MTW, TM>(
-        [&](int row) { return row_ptr<R>(a, wk.r0 + p0 + row); }, mp, xr);
     sf_f32x4 acc[MTW][NT];
-    stream_gemm<NT, MTW, KS, NB>(w, xr, wave / TM, active, smem, acc);
+    auto row_of = [&](int row) { return row_ptr<R>(a, wk.r0 + p0 + row); };
+    if constexpr (KS == 1 && MTW == 1) {
+      const uint16_t* xr[4];
+      const bool active = a_rows_staged(row_of, mp, xr);
+      stream_gemm<NT, MTW, KS, NB, 4>(w, xr, 0, active, smem,
+                                       smem + 2 * 16 * NT * kRowBytes + wave * kStageBytes, acc);
+    } else {
+      const uint16_t* xr[MTW];
+      const bool active = a_rows<MTW, TM>(row_of, mp, xr);
+      stream_gemm<NT, MTW, KS, NB, MTW>(w, xr, wave / TM, active, smem, nullptr, acc);
+    }
     bool owner = true;
     if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
     if (!owner) continue;
@@ -364,7 +446,8 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
 // understated) runs in passes of the class's largest split.
 template <Resolve R, int MC, int NB, int NT>
 __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const SwigluArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * 16 * NT * kRowBytes];
+  __shared__ __attribute__((aligned(16)))
+  char smem[2 * 16 * NT * kRowBytes + (MC >= 2 ? kWaves * kStageBytes : 0)];
   const int tiles = a.I / (8 * NT);
   const int j = blockIdx.x / tiles;
   const int tile = blockIdx.x - j * tiles;
@@ -402,7 +485,7 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
     const bool active = a_rows<MTW, TM>(
         [&](int row) { return a.act + static_cast<int64_t>(wk.r0 + p0 + row) * I; }, mp, ar);
     sf_f32x4 acc[MTW][NT];
-    stream_gemm<NT, MTW, KS, NB>(w, ar, wave / TM, active, smem, acc);
+    stream_gemm<NT, MTW, KS, NB, MTW>(w, ar, wave / TM, active, smem, nullptr, acc);
     bool owner = true;
     if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
     if (!owner) continue;

@@ -288,7 +288,8 @@ def test_grouped_swiglu_row_classes_streams_and_table(device):
     assert not out[r0].any()
 
 
-@pytest.mark.parametrize("H,I,m", [(4, 3, 2), (32, 16, 5), (96, 64, 70), (2048, 768, 130)])
+@pytest.mark.parametrize("H,I,m", [(4, 3, 2), (32, 16, 5), (96, 64, 70), (2048, 768, 48),
+                                   (2048, 768, 130)])
 def test_expert_swiglu_generic_and_mfma_paths(device, H, I, m):
     g = torch.Generator("cpu").manual_seed(H + I + m)
     x = torch.randn(m, H, generator=g).to(torch.bfloat16)
