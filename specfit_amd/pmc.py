@@ -65,6 +65,13 @@ def _tile_width(name: str) -> int:
     return int(m.group(1).split(",")[-1])
 
 
+def _is_table(name: str) -> bool:
+    """A slot-table K3 dispatch (Resolve 1): one workgroup set per table
+    entry, whether or not that expert has rows."""
+    m = re.search(r"Resolve\)(\d)", name)
+    return bool(m) and m.group(1) == "1"
+
+
 def _k3_weight_bytes(name: str, grid: int) -> int | None:
     if "gateup_mfma_kernel" in name:
         cols = 8 * _tile_width(name)
@@ -183,16 +190,22 @@ def summarize_trace(trace_dir: str, command: str | None = None,
     phases = ((("in-step", [r for i, r in k3 if cal and i < cal[0]]),
                ("all-resident", [r for i, r in k3 if cal and i > cal[-1]])) if split
               else (("all", [r for _, r in k3]),))
+    dur = lambda rs: sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rs) / len(rs) / 1e3
     for label, sel in phases:
-        g = [r for r in sel if "gateup" in r["Kernel_Name"]]
-        d = [r for r in sel if "down_mfma" in r["Kernel_Name"]]
-        if not g or len(g) != len(d):
-            continue
-        dur = lambda rs: sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rs) / len(rs) / 1e3
-        wb = sum(_k3_weight_bytes(r["Kernel_Name"], int(r["Grid_Size_X"])) for r in sel) / len(g)
-        t = dur(g) + dur(d)
-        lines.append(f"| {label} | {len(g)} | {dur(g):.2f} | {dur(d):.2f} | {t:.2f} | "
-                     f"{wb / 1e6:.2f} | {wb / (t * 1e-6) / 1e9:.0f} |")
+        for table in (False, True):
+            part = [r for r in sel if _is_table(r["Kernel_Name"]) == table]
+            g = [r for r in part if "gateup" in r["Kernel_Name"]]
+            d = [r for r in part if "down_mfma" in r["Kernel_Name"]]
+            if not g or len(g) != len(d):
+                continue
+            t = dur(g) + dur(d)
+            if table:  # the grid covers every table entry, not the experts computed
+                lines.append(f"| {label}, slot table | {len(g)} | {dur(g):.2f} | {dur(d):.2f} | "
+                             f"{t:.2f} | n/a | n/a |")
+                continue
+            wb = sum(_k3_weight_bytes(r["Kernel_Name"], int(r["Grid_Size_X"])) for r in part) / len(g)
+            lines.append(f"| {label} | {len(g)} | {dur(g):.2f} | {dur(d):.2f} | {t:.2f} | "
+                         f"{wb / 1e6:.2f} | {wb / (t * 1e-6) / 1e9:.0f} |")
     return "\n".join(lines) + "\n"
 
 

@@ -106,6 +106,9 @@ def test_trace_summary_averages_k3_launches_per_phase(tmp_path):
     add(CAL, 1 << 20, 90_000)
     add(_name("gateup", 2), _grid("gateup", 2, 45), 55_000)
     add(_name("down", 2), _grid("down", 2, 45), 33_000)
+    table = lambda n: n.replace("Resolve)0", "Resolve)1")  # slot-table launch over 128 entries
+    add(table(_name("gateup", 2, 0)), _grid("gateup", 2, 128), 80_000)
+    add(table(_name("down", 2, 0)), _grid("down", 2, 128), 40_000)
     with open(d / "k3_kernel_trace.csv", "w", newline="") as fh:
         w = csv.DictWriter(fh, fieldnames=list(rows[0]))
         w.writeheader()
@@ -117,6 +120,8 @@ def test_trace_summary_averages_k3_launches_per_phase(tmp_path):
     text = pmc.summarize_trace(str(d))
     lines = {l.split("|")[1].strip(): l for l in text.splitlines()
              if l.startswith("| in-step") or l.startswith("| all-resident")}
+    table_row = [c.strip() for c in lines["all-resident, slot table"].split("|")[1:-1]]
+    assert table_row[1:] == ["1", "80.00", "40.00", "120.00", "n/a", "n/a"]
     in_step = [c.strip() for c in lines["in-step"].split("|")[1:-1]]
     assert in_step[1:5] == ["3", "10.00", "6.00", "16.00"]
     assert float(in_step[5]) == pytest.approx(2 * (GATEUP_BYTES + DOWN_BYTES) / 1e6, abs=0.01)
