@@ -135,9 +135,10 @@ int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
  *                   computes every row; with a value below some expert's
  *                   row count that expert's fp32 summation order is the one
  *                   of a smaller expert.
- * The MFMA kernels cover the Qwen3-30B-A3B expert shape (hidden 2048,
- * intermediate 768) with 16-byte aligned buffers; other shapes run fp32
- * loop kernels with the same rounding points.  The fp32 summation order of
+ * The MFMA kernels cover the Qwen3-30B-A3B (hidden 2048, intermediate 768)
+ * and Qwen3-235B-A22B (hidden 4096, intermediate 1536) expert shapes with
+ * 16-byte aligned buffers; other shapes run fp32 loop kernels with the same
+ * rounding points.  The fp32 summation order of
  * an output depends on the shape and on its expert's row count only.
  *   expert_ids      host int32 [n_experts]: experts computed by this call
  *   expert_weights  host uint64 [n_experts]: device address of each expert's

@@ -6,8 +6,8 @@
 // with GU = packed[0:2IH] as [2I, H] and D = packed[2IH:] as [H, I].
 //
 // At verification sizes an expert sees m <= a few dozen rows, so each weight
-// element is used m times and the GEMMs are bound by streaming the 9 MiB of
-// expert weights from HBM.  Every weight byte is read from HBM once.
+// element is used m times and the GEMMs are bound by streaming the expert's
+// weights (9 MiB for Qwen3-30B-A3B) from HBM.  Every weight byte is read from HBM once.
 //
 // Weight stream.  A workgroup owns a slab of 32 weight rows in a wide launch
 // (phase 1: the 16 gate + 16 up rows of 16 activation columns; phase 2: 32
@@ -22,12 +22,13 @@
 // registers two blocks ahead, each block's right after the MFMAs that used
 // the previous contents: in MFMA fragment layout, except in gate/up's split
 // for 33..64 rows, which loads them row-contiguously and passes them through
-// a per-wavefront LDS region (see mfma_block_staged).  The block count is a compile-time constant of the
-// expert shape, so the loop is unrolled and every load is unconditional: the
-// compiler's vector-memory wait counts are then exact (they are in-order
-// counters; a conditional load would force a full drain).  Scheduling
-// barriers keep the loads in issue order, so registers hold only the blocks
-// in flight.
+// a per-wavefront LDS region (see mfma_block_staged).  The block count is a
+// compile-time constant of the expert shape (built for the Qwen3-30B-A3B and
+// Qwen3-235B-A22B experts), so the loop is unrolled and every load is
+// unconditional: the compiler's vector-memory wait counts are then exact
+// (they are in-order counters; a conditional load would force a full drain).
+// Scheduling barriers keep the loads in issue order, so registers hold only
+// the blocks in flight.
 //
 // Work split of a pass.  The 4 wavefronts cover TM sixteen-row token tiles x
 // KS k-slices (TM * KS = 4), chosen per workgroup from its expert's row
@@ -577,24 +578,26 @@ __global__ __launch_bounds__(kThreads) void down_generic_kernel(const SwigluArgs
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Compiled (H, I) block counts of the MFMA path: Qwen3-30B-A3B experts
-// (H = 2048, I = 768).  Other shapes take the generic kernels.
-constexpr int kNbGateup = 8;
-constexpr int kNbDown = 3;
+// Compiled (H, I) shapes of the MFMA path, as 256-k block counts of a
+// gate/up row (H / 256) and of a down row (I / 256): the Qwen3-30B-A3B
+// expert (H = 2048, I = 768) and the Qwen3-235B-A22B expert (H = 4096,
+// I = 1536).  Other shapes take the generic kernels.
+enum class Shape { kGeneric, k2048x768, k4096x1536 };
 
-bool mfma_shape_ok(int H, int I) {
-  return H == kNbGateup * kBlockK && I == kNbDown * kBlockK;
+Shape mfma_shape(int H, int I) {
+  if (H == 8 * kBlockK && I == 3 * kBlockK) return Shape::k2048x768;
+  if (H == 16 * kBlockK && I == 6 * kBlockK) return Shape::k4096x1536;
+  return Shape::kGeneric;
 }
 
-template <Resolve R, int MC, int NT>
+template <Resolve R, int MC, int NT, int NBG, int NBD>
 int launch_mfma(const SwigluArgs& a, int groups, hipStream_t s) {
   const long long g1 = static_cast<long long>(groups) * (a.I / (8 * NT));
   const long long g2 = static_cast<long long>(groups) * (a.H / (16 * NT));
   if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL) return SF_ERR_UNSUPPORTED_SHAPE;
-  gateup_mfma_kernel<R, MC, kNbGateup, NT>
-      <<<dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, s>>>(a);
+  gateup_mfma_kernel<R, MC, NBG, NT><<<dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
-  down_mfma_kernel<R, MC, kNbDown, NT><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
+  down_mfma_kernel<R, MC, NBD, NT><<<dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
   return SF_OK;
 }
@@ -615,23 +618,27 @@ bool narrow_tiles(int groups, int max_rows) {
   return max_rows <= 16 && groups <= kNarrowMaxGroups;
 }
 
-template <Resolve R, int NT>
+template <Resolve R, int NT, int NBG, int NBD>
 int launch_class(const SwigluArgs& a, int groups, int max_rows, hipStream_t s) {
-  if (max_rows <= 16) return launch_mfma<R, 0, NT>(a, groups, s);
-  if (max_rows <= 32) return launch_mfma<R, 1, NT>(a, groups, s);
-  if (max_rows <= 64) return launch_mfma<R, 2, NT>(a, groups, s);
-  return launch_mfma<R, 3, NT>(a, groups, s);
+  if (max_rows <= 16) return launch_mfma<R, 0, NT, NBG, NBD>(a, groups, s);
+  if (max_rows <= 32) return launch_mfma<R, 1, NT, NBG, NBD>(a, groups, s);
+  if (max_rows <= 64) return launch_mfma<R, 2, NT, NBG, NBD>(a, groups, s);
+  return launch_mfma<R, 3, NT, NBG, NBD>(a, groups, s);
+}
+
+template <Resolve R, int NBG, int NBD>
+int launch_width(const SwigluArgs& a, int groups, int max_rows, hipStream_t s) {
+  if (narrow_tiles(groups, max_rows)) return launch_class<R, 1, NBG, NBD>(a, groups, max_rows, s);
+  return launch_class<R, 2, NBG, NBD>(a, groups, max_rows, s);
 }
 
 // max_rows bounds the rows of any expert of the launch; it picks the row
 // class of the build.
 template <Resolve R>
-int launch(const SwigluArgs& a, int groups, bool mfma, int max_rows, hipStream_t s) {
+int launch(const SwigluArgs& a, int groups, Shape shape, int max_rows, hipStream_t s) {
   if (groups <= 0) return SF_OK;
-  if (mfma) {
-    if (narrow_tiles(groups, max_rows)) return launch_class<R, 1>(a, groups, max_rows, s);
-    return launch_class<R, 2>(a, groups, max_rows, s);
-  }
+  if (shape == Shape::k2048x768) return launch_width<R, 8, 3>(a, groups, max_rows, s);
+  if (shape == Shape::k4096x1536) return launch_width<R, 16, 6>(a, groups, max_rows, s);
   gateup_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
   SF_LAUNCH_CHECK();
   down_generic_kernel<R><<<dim3(groups), dim3(kThreads), 0, s>>>(a);
@@ -662,12 +669,12 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
   if (!hidden || !perm_pos || !offsets || !expert_ids || !expert_weights ||
       !act_workspace || !out_rows)
     return SF_ERR_INVALID_ARGUMENT;
-  bool mfma = mfma_shape_ok(hidden_size, intermediate_size) && aligned16(hidden) &&
-              aligned16(act_workspace);
+  bool aligned = aligned16(hidden) && aligned16(act_workspace);
   for (int i = 0; i < n_experts; ++i) {
     if (expert_ids[i] < 0 || expert_weights[i] == 0) return SF_ERR_INVALID_ARGUMENT;
-    if (expert_weights[i] & 15u) mfma = false;
+    if (expert_weights[i] & 15u) aligned = false;
   }
+  const Shape shape = aligned ? mfma_shape(hidden_size, intermediate_size) : Shape::kGeneric;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   for (int base = 0; base < n_experts; base += kMaxListExperts) {
     SwigluArgs a{};
@@ -686,7 +693,7 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
       a.expert[i] = expert_ids[base + i];
       a.wptr[i] = expert_weights[base + i];
     }
-    rc = launch<Resolve::kList>(a, a.n, mfma, max_rows, s);
+    rc = launch<Resolve::kList>(a, a.n, shape, max_rows, s);
     if (rc) return rc;
   }
   return SF_OK;
@@ -707,9 +714,9 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
   if (!hidden || !perm_pos || !offsets || !slot_of_expert || !slot_base ||
       !act_workspace || !out_rows)
     return SF_ERR_INVALID_ARGUMENT;
-  const bool mfma = mfma_shape_ok(hidden_size, intermediate_size) && aligned16(hidden) &&
-                    aligned16(act_workspace) && aligned16(slot_base) &&
-                    (slot_stride_elems % 8 == 0);
+  const bool aligned = aligned16(hidden) && aligned16(act_workspace) && aligned16(slot_base) &&
+                       (slot_stride_elems % 8 == 0);
+  const Shape shape = aligned ? mfma_shape(hidden_size, intermediate_size) : Shape::kGeneric;
   SwigluArgs a{};
   a.hidden = static_cast<const uint16_t*>(hidden);
   a.perm_pos = perm_pos;
@@ -725,7 +732,7 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
   a.slot_of_expert = slot_of_expert;
   a.slot_base = static_cast<const uint16_t*>(slot_base);
   a.slot_stride = slot_stride_elems;
-  return launch<Resolve::kTable>(a, num_experts, mfma, max_rows,
+  return launch<Resolve::kTable>(a, num_experts, shape, max_rows,
                                  reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -737,9 +744,9 @@ extern "C" int sf_expert_swiglu(const void* rows, int m, int64_t row_stride,
     return SF_ERR_INVALID_ARGUMENT;
   if (m == 0) return SF_OK;
   if (!rows || !packed_weights || !act_workspace || !out) return SF_ERR_INVALID_ARGUMENT;
-  const bool mfma = mfma_shape_ok(hidden_size, intermediate_size) && aligned16(rows) &&
-                    (row_stride % 8 == 0) && aligned16(packed_weights) &&
-                    aligned16(act_workspace);
+  const bool aligned = aligned16(rows) && (row_stride % 8 == 0) && aligned16(packed_weights) &&
+                       aligned16(act_workspace);
+  const Shape shape = aligned ? mfma_shape(hidden_size, intermediate_size) : Shape::kGeneric;
   SwigluArgs a{};
   a.hidden = static_cast<const uint16_t*>(rows);
   a.act = static_cast<uint16_t*>(act_workspace);
@@ -751,5 +758,5 @@ extern "C" int sf_expert_swiglu(const void* rows, int m, int64_t row_stride,
   a.dense_m = m;
   a.n = 1;
   a.wptr[0] = reinterpret_cast<uint64_t>(packed_weights);
-  return launch<Resolve::kDense>(a, 1, mfma, m, reinterpret_cast<hipStream_t>(stream));
+  return launch<Resolve::kDense>(a, 1, shape, m, reinterpret_cast<hipStream_t>(stream));
 }

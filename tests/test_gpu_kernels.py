@@ -288,8 +288,37 @@ def test_grouped_swiglu_row_classes_streams_and_table(device):
     assert not out[r0].any()
 
 
+def test_grouped_swiglu_qwen3_235b_shape(device):
+    """The MFMA path's second compiled expert shape (Qwen3-235B-A22B: hidden
+    4096, intermediate 1536), with Zipf-skewed experts spanning the row
+    classes: one grouped launch gives the rows of one-expert launches bit
+    for bit, and the bf16-eager oracle's rows within tolerance."""
+    E, T, K = 8, 96, 4
+    layer = make_layer(seed=3, hidden_size=4096, intermediate_size=1536, num_experts=E,
+                       top_k=K, zipf_s=1.1)
+    H, I = 4096, 1536
+    hidden = make_hidden(T, H, seed=4, zipf_fold=True)
+    h_dev, idx, w, plan, rows, slots = _moe_rows(device, layer, hidden, K, list(range(E)))
+    ms = [int(c) for c in plan.fetch_counts()[0][:E]]
+    print(f"235b-shape case rows per expert {ms}", flush=True)
+    assert min(ms) <= 32 and max(ms) > 64
+    wflat = w.reshape(-1).contiguous()
+    act = torch.empty((T * K, I), dtype=torch.bfloat16, device=device)
+    one = torch.zeros_like(rows)
+    for e in range(E):
+        if ms[e]:
+            ops.grouped_swiglu(h_dev, plan, wflat, [e], [slots[e]], H, I, act, one)
+    torch.cuda.synchronize()
+    assert torch.equal(one, rows)
+    x = oracle.bf16_float(_bits(hidden))
+    experts = {e: oracle.bf16_float(_bits(layer.experts[e])) for e in range(E)}
+    ref_rows, *_ = oracle.moe_rows_bf16(x, idx.cpu().numpy(), oracle.bf16_float(_bits(w)), experts,
+                                        H, I, E)
+    np.testing.assert_allclose(oracle.bf16_float(_bits(rows)), ref_rows, rtol=1.6e-2, atol=1.6e-2)
+
+
 @pytest.mark.parametrize("H,I,m", [(4, 3, 2), (32, 16, 5), (96, 64, 70), (2048, 768, 48),
-                                   (2048, 768, 130)])
+                                   (2048, 768, 130), (4096, 1536, 20), (4096, 1536, 70)])
 def test_expert_swiglu_generic_and_mfma_paths(device, H, I, m):
     g = torch.Generator("cpu").manual_seed(H + I + m)
     x = torch.randn(m, H, generator=g).to(torch.bfloat16)
