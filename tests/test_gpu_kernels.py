@@ -59,6 +59,7 @@ def test_router_bitexact_zipf_biased(device):
     (5, 100, 60, 4, True),    # H not a multiple of 8: scalar path
     (3, 8192, 256, 32, True), # largest expert count / top-k
     (7, 2048, 128, 8, False),
+    (20, 4096, 128, 8, True), # Qwen3-235B-A22B router (8 chunks per lane)
 ])
 def test_router_bitexact_other_shapes(device, T, H, E, K, renorm):
     _router_case(device, T, H, E, K, renorm, 21)
