@@ -102,7 +102,6 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
   }
 
   // Pass 2: stable scatter, chunk by chunk.
-  const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (SF_WAVE - lane));
   for (int base = 0; base < N; base += kDispatchThreads) {
     const int i = base + tid;
     int e = -1;
@@ -110,17 +109,25 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
       const int64_t v = base == 0 ? first : idx[i];
       e = (v >= 0 && v < E) ? static_cast<int>(v) : -1;
     }
-    const bool valid = e >= 0;
-    int rank = 0;
-    uint64_t pending = __ballot(valid);
+    // One round per distinct id of the wavefront: the lowest pending lane
+    // leads, its id is read with a scalar lane read (no LDS round trip on
+    // the loop's dependency chain), and the lanes holding it take their
+    // rank (lanes below with the same id, mbcnt) and group size.
+    int rank = 0, group = 0;
+    uint64_t pending = __ballot(e >= 0);
     while (pending) {
       const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
-      const int le = __shfl(e, leader, SF_WAVE);
-      const uint64_t same = __ballot(valid && e == le);
-      if (valid && e == le) rank = __popcll(same & lanes_below);
-      if (lane == leader) s_wave_count[wave][le] = __popcll(same);
+      const int le = __builtin_amdgcn_readlane(e, leader);
+      const uint64_t same = __ballot(e == le);
+      if (e == le) {
+        rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(same >> 32),
+                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(same), 0));
+        group = __popcll(same);
+      }
       pending &= ~same;
     }
+    const bool valid = e >= 0;
+    if (valid && rank == 0) s_wave_count[wave][e] = group;
     __syncthreads();
     // Exclusive prefix over the wavefronts that hold routes in this chunk
     // (the others' counts are zero), per expert, continuing the running
