@@ -131,7 +131,15 @@ __device__ __forceinline__ sf_f32x4 mfma16(uint4 a, uint4 b, sf_f32x4 c) {
 
 // ------------------------------------------------------ streaming core --
 constexpr int kSteps = kBlockK / 32;  // MFMA k-steps per block
-constexpr int kDepth = 2;             // blocks in flight ahead of the one in use
+// Blocks in flight ahead of the one in use: 2, and 3 for down's <= 16-row
+// split (KS = 4), whose slab is only I / 256 blocks long (3 at I = 768), so
+// its workgroups issue every load at the start (16-token all-resident
+// launch: down 45.6 -> 44.9 us over the slot table, 49.9 -> 47.6 us over
+// listed experts).  Measured slower elsewhere: gate/up at 3 (83.7 -> 85.5
+// us), and down's wider splits at 3 (64-token all-resident down 33.9 -> 39.3
+// us: their A fragments of a third block cost registers).
+constexpr int kDepth = 2;
+constexpr int kDownDepth = 3;
 
 // Keeps the compiler's scheduler from moving instructions across this point,
 // so loads stay in issue order and registers hold only blocks in flight.
@@ -258,12 +266,12 @@ __device__ __forceinline__ void mfma_block_staged(const char* tile, char* stage,
 // acc = X . W^T over k-slice `slice` of KS (SP = kSteps/KS k-steps of each of
 // the NB blocks).  active: wave-uniform, false when the wavefront's tiles
 // have no rows (its A loads then hit one cache line, see a_rows).
-template <int NT, int MTW, int KS, int NB, int NP>
+template <int NT, int MTW, int KS, int NB, int NP, int DP = kDepth>
 __device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* const (&xr)[NP],
                                             int slice, bool active, char* smem, char* stage,
                                             sf_f32x4 (&acc)[MTW][NT]) {
   constexpr bool kStaged = KS == 1 && MTW == 1 && NP == 4;
-  static_assert(NB >= kDepth, "fewer blocks than the prefetch depth");
+  static_assert(NB >= DP, "fewer blocks than the prefetch depth");
   constexpr int SP = kSteps / KS;
   constexpr int kTile = 16 * NT * kRowBytes;
   const int lane = threadIdx.x & (SF_WAVE - 1);
@@ -273,21 +281,21 @@ __device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* c
   for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-  uint4 wr[kDepth][2 * NT];
-  uint4 xq[kDepth][MTW][SP];
+  uint4 wr[DP][2 * NT];
+  uint4 xq[DP][MTW][SP];
 #pragma unroll
-  for (int d = 0; d < kDepth; ++d) {
+  for (int d = 0; d < DP; ++d) {
     load_w<NT>(w, d, lane, wave, wr[d]);
     if constexpr (kStaged) load_x_rows(xr, d, xq[d]);
     else load_x<MTW, SP>(xr, d, s0, xq[d]);
   }
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    const int d = b % kDepth;
+    const int d = b % DP;
     char* tile = smem + (b & 1) * kTile;
     store_w<NT>(tile, lane, wave, wr[d]);
     SF_SCHED_FENCE();
-    if (b + kDepth < NB) load_w<NT>(w, b + kDepth, lane, wave, wr[d]);
+    if (b + DP < NB) load_w<NT>(w, b + DP, lane, wave, wr[d]);
     SF_SCHED_FENCE();
     __syncthreads();  // tile b visible; tile b-1's reads are done
     if constexpr (kStaged) {
@@ -296,9 +304,9 @@ __device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* c
       if (active) mfma_block<NT, MTW, SP>(tile, s0, xq[d], lane, acc);
     }
     SF_SCHED_FENCE();
-    if (b + kDepth < NB) {
-      if constexpr (kStaged) load_x_rows(xr, b + kDepth, xq[d]);
-      else load_x<MTW, SP>(xr, b + kDepth, s0, xq[d]);
+    if (b + DP < NB) {
+      if constexpr (kStaged) load_x_rows(xr, b + DP, xq[d]);
+      else load_x<MTW, SP>(xr, b + DP, s0, xq[d]);
     }
     SF_SCHED_FENCE();
   }
@@ -486,7 +494,7 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
     const bool active = a_rows<MTW, TM>(
         [&](int row) { return a.act + static_cast<int64_t>(wk.r0 + p0 + row) * I; }, mp, ar);
     sf_f32x4 acc[MTW][NT];
-    stream_gemm<NT, MTW, KS, NB, MTW>(w, ar, wave / TM, active, smem, nullptr, acc);
+    stream_gemm<NT, MTW, KS, NB, MTW, (KS == 4 && NB >= kDownDepth ? kDownDepth : kDepth)>(w, ar, wave / TM, active, smem, nullptr, acc);
     bool owner = true;
     if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
     if (!owner) continue;
