@@ -45,11 +45,15 @@ __device__ __forceinline__ float dot8_acc(uint4 hv, uint4 wv, float acc) {
 // Softmax + top-k + renorm over s_logit[0..E) by one wavefront.  Lane l
 // reads only experts l, l+64, ... of s_logit.  Each top-k round takes the
 // wave maximum of the unselected probabilities and the lowest expert id
-// holding it (ballots per 64-expert slice, lowest lane first).
+// holding it (ballots per 64-expert slice, lowest lane first).  The rounds
+// compare the probabilities' bit patterns as integers: p is in [0, 1] for
+// finite logits, so integer order is float order and equal bits are equal
+// values; -1 marks a slot past E or an expert already taken.  Lane r keeps round r's value and id,
+// so the renormalisation divides in K lanes at once and the stores are
+// contiguous.
 template <int J>  // experts per lane: E <= 64 * J
 __device__ void softmax_topk_wave(const float* s_logit, int E, int K, int renorm,
-                                  uint16_t* topw, int64_t* topi, float* s_val,
-                                  int* s_id) {
+                                  uint16_t* topw, int64_t* topi) {
   const int lane = threadIdx.x & (SF_WAVE - 1);
   float m = -__builtin_inff();
 #pragma unroll
@@ -71,42 +75,37 @@ __device__ void softmax_topk_wave(const float* s_logit, int E, int K, int renorm
     }
   }
   const float total = sf_wave_sum(part);
-  float p[J];
-  bool live[J];
+  int key[J];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    int e = lane + SF_WAVE * j;
-    live[j] = e < E;
-    p[j] = live[j] ? x[j] / total : 0.0f;
-  }
+  for (int j = 0; j < J; ++j) key[j] = lane + SF_WAVE * j < E ? __float_as_int(x[j] / total) : -1;
+  float mine = 0.0f;
+  int mine_id = 0;
   for (int r = 0; r < K; ++r) {
-    float lb = -1.0f;  // probabilities are >= 0
+    int lk = key[0];
 #pragma unroll
-    for (int j = 0; j < J; ++j)
-      if (live[j] && p[j] > lb) lb = p[j];
-    const float bp = sf_wave_max(lb);
-    int be = 0x7fffffff;
+    for (int j = 1; j < J; ++j) lk = max(lk, key[j]);
+    const int bk = sf_wave_max_int(lk);
+    int be = -1;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const unsigned long long hit = __ballot(live[j] && p[j] == bp);
-      if (be == 0x7fffffff && hit) be = SF_WAVE * j + __ffsll(hit) - 1;
+      const unsigned long long hit = __ballot(key[j] == bk);
+      if (be < 0 && hit) be = SF_WAVE * j + __ffsll(hit) - 1;
     }
 #pragma unroll
     for (int j = 0; j < J; ++j)
-      if (be == lane + SF_WAVE * j) live[j] = false;
-    if (lane == 0) {
-      s_val[r] = bp;
-      s_id[r] = be;
+      if (be == lane + SF_WAVE * j) key[j] = -1;
+    if (lane == r) {
+      mine = __int_as_float(bk);
+      mine_id = be;
     }
   }
-  if (lane == 0) {
-    float sum = 0.0f;
-    for (int r = 0; r < K; ++r) sum += s_val[r];
-    for (int r = 0; r < K; ++r) {
-      float v = renorm ? s_val[r] / sum : s_val[r];
-      topw[r] = sf_f32_to_bf16(v);
-      topi[r] = static_cast<int64_t>(s_id[r]);
-    }
+  float sum = 0.0f;
+  if (renorm)
+    for (int r = 0; r < K; ++r) sum += sf_readlane(mine, r);
+  if (lane < K) {
+    const float v = renorm ? mine / sum : mine;
+    topw[lane] = sf_f32_to_bf16(v);
+    topi[lane] = static_cast<int64_t>(mine_id);
   }
 }
 
@@ -189,8 +188,6 @@ __global__ __launch_bounds__(kSelectWaves * SF_WAVE) void router_select_kernel(
     const uint16_t* __restrict__ logits, int T, int E, int K, int renorm,
     uint16_t* __restrict__ topw, int64_t* __restrict__ topi) {
   __shared__ float s_logit[kSelectWaves][SF_MAX_EXPERTS];
-  __shared__ float s_val[kSelectWaves][SF_MAX_TOPK];
-  __shared__ int s_id[kSelectWaves][SF_MAX_TOPK];
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int t = blockIdx.x * kSelectWaves + wave;
@@ -199,7 +196,7 @@ __global__ __launch_bounds__(kSelectWaves * SF_WAVE) void router_select_kernel(
   for (int e = lane; e < E; e += SF_WAVE)
     s_logit[wave][e] = sf_bf16_to_f32(logits[static_cast<size_t>(t) * E + e]);
   softmax_topk_wave<J>(s_logit[wave], E, K, renorm, topw + static_cast<size_t>(t) * K,
-                       topi + static_cast<size_t>(t) * K, s_val[wave], s_id[wave]);
+                       topi + static_cast<size_t>(t) * K);
 }
 
 // Scalar path for any hidden_size / alignment: same summation order.
@@ -208,8 +205,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_scalar_kernel(
     int E, int K, int renorm, uint16_t* __restrict__ logits,
     uint16_t* __restrict__ topw, int64_t* __restrict__ topi) {
   __shared__ float s_logit[SF_MAX_EXPERTS];
-  __shared__ float s_val[SF_MAX_TOPK];
-  __shared__ int s_id[SF_MAX_TOPK];
   const int t = blockIdx.x;
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
@@ -235,7 +230,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_scalar_kernel(
   if (wave == 0)
     softmax_topk_wave<SF_MAX_EXPERTS / SF_WAVE>(s_logit, E, K, renorm,
                                                 topw + static_cast<size_t>(t) * K,
-                                                topi + static_cast<size_t>(t) * K, s_val, s_id);
+                                                topi + static_cast<size_t>(t) * K);
 }
 
 }  // namespace

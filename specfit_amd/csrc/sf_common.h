@@ -92,6 +92,16 @@ __device__ __forceinline__ float sf_wave_max(float x) {
                fmaxf(sf_readlane(x, 32), sf_readlane(x, 48)));
 }
 
+// Maximum of the 64 lanes' x (signed integers), wave-uniform.
+__device__ __forceinline__ int sf_wave_max_int(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x141, 0xf, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x140, 0xf, 0xf, false));
+  return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
 #define SF_HIP_CHECK(expr)                                        \
   do {                                                            \
     hipError_t sf_err__ = (expr);                                 \
