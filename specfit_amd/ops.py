@@ -31,6 +31,7 @@ def _hip():
         lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
                                             ctypes.c_void_p]
         lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
         _hip_runtime = lib
     return _hip_runtime
 
@@ -65,6 +66,43 @@ class TimingEvent:
         if self._ev and _hip_runtime is not None:
             _hip_runtime.hipEventDestroy(self._ev)
             self._ev = ctypes.c_void_p()
+
+
+_HIP_EVENT_DISABLE_TIMING = 0x2  # hip_runtime_api.h
+
+
+class HostWaitEvent:
+    """A HIP event (no timing) recorded on a raw stream handle for the host
+    to wait on, as torch.cuda.Event.record + synchronize but without a
+    Stream object or a fresh event per record: handles come from a pool and
+    go back to it when the wrapper is dropped (re-recording a handle whose
+    earlier record is still pending is allowed)."""
+
+    _pool: list = []
+    __slots__ = ("_ev",)
+
+    def __init__(self, stream_handle: int) -> None:
+        self._ev = None
+        ev = self._pool.pop() if self._pool else None
+        if ev is None:
+            ev = ctypes.c_void_p()
+            rc = _hip().hipEventCreateWithFlags(ctypes.byref(ev), _HIP_EVENT_DISABLE_TIMING)
+            if rc:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+        self._ev = ev
+        rc = _hip().hipEventRecord(ev, ctypes.c_void_p(stream_handle))
+        if rc:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def synchronize(self) -> None:
+        rc = _hip().hipEventSynchronize(self._ev)
+        if rc:
+            raise RuntimeError(f"hipEventSynchronize failed ({rc})")
+
+    def __del__(self) -> None:
+        if self._ev is not None:
+            self._pool.append(self._ev)
+            self._ev = None
 
 
 class LaunchRecorder:
@@ -305,13 +343,13 @@ def dispatch(index: torch.Tensor, num_experts: int, *,
             plan.count_list = host_meta[0].tolist()
         return plan
     handle = _stream_handle(stream, dev)
-    rc = _native.lib().sf_dispatch(_ptr(index), T, K, int(num_experts), _ptr(meta[0]),
-                                   _ptr(meta[1]), _ptr(perm), _ptr(inv), _ptr(host_meta), handle)
+    counts_ptr = meta.data_ptr()  # row 0; row 1 (offsets) follows E + 1 int32 later
+    rc = _native.lib().sf_dispatch(_ptr(index), T, K, int(num_experts), counts_ptr,
+                                   counts_ptr + 4 * (num_experts + 1), _ptr(perm), _ptr(inv),
+                                   _ptr(host_meta), handle)
     _native.check(rc, "sf_dispatch")
     if host_meta is not None:
-        ev = torch.cuda.Event()
-        ev.record(stream if stream is not None else torch.cuda.current_stream(dev))
-        plan._counts_event = (ev, host_meta)
+        plan._counts_event = (HostWaitEvent(handle), host_meta)
     return plan
 
 

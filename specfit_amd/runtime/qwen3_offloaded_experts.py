@@ -322,9 +322,12 @@ class Qwen3OffloadedExperts(nn.Module):
             return None, ()
         num_experts = self.num_experts()
         plan = _dispatch(top_k_index, num_experts, self._counts_staging(num_experts))
+        # The row buffers do not depend on the counts: allocate them while
+        # the device routes.
+        routes = self._new_routes(hidden_states, top_k_weights, plan)
         counts = self._read_counts(plan, top_k_index, num_experts)
         active = tuple(compress(range(num_experts), counts))
-        return self._new_routes(hidden_states, top_k_weights, plan), active
+        return routes, active
 
     def _counts_staging(self, num_experts: int) -> torch.Tensor:
         if self._host_counts is None:
