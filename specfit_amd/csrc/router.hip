@@ -48,9 +48,9 @@ __device__ __forceinline__ float dot8_acc(uint4 hv, uint4 wv, float acc) {
 // holding it (ballots per 64-expert slice, lowest lane first).  The rounds
 // compare the probabilities' bit patterns as integers: p is in [0, 1] for
 // finite logits, so integer order is float order and equal bits are equal
-// values; -1 marks a slot past E or an expert already taken.  Lane r keeps round r's value and id,
-// so the renormalisation divides in K lanes at once and the stores are
-// contiguous.
+// values; -1 marks a slot past E or an expert already taken.  Lane r keeps
+// round r's value and id, so the renormalisation divides in K lanes at once
+// and the stores are contiguous.
 template <int J>  // experts per lane: E <= 64 * J
 __device__ void softmax_topk_wave(const float* s_logit, int E, int K, int renorm,
                                   uint16_t* topw, int64_t* topi) {
