@@ -100,7 +100,12 @@ def _dispatch_case(device, idx: np.ndarray, E: int):
 
 
 @pytest.mark.parametrize("T,K,E,seed", [(64, 8, 128, 0), (1, 8, 128, 1), (16, 8, 128, 2),
-                                        (200, 8, 128, 3), (513, 7, 256, 4), (4, 2, 4, 5)])
+                                        (200, 8, 128, 3), (513, 7, 256, 4), (4, 2, 4, 5),
+                                        # chunk and kernel-width boundaries: 256 routes
+                                        # (last 256-thread case), 264, 1024 (one full
+                                        # 1024 chunk), 1032 (a second chunk of 8)
+                                        (32, 8, 128, 6), (33, 8, 128, 7), (128, 8, 256, 8),
+                                        (129, 8, 64, 9)])
 def test_dispatch_bitexact(device, T, K, E, seed):
     rng = np.random.default_rng(seed)
     idx = rng.integers(0, E, size=(T, K)).astype(np.int64)
