@@ -60,6 +60,10 @@ def test_router_bitexact_zipf_biased(device):
     (3, 8192, 256, 32, True), # largest expert count / top-k
     (7, 2048, 128, 8, False),
     (20, 4096, 128, 8, True), # Qwen3-235B-A22B router (8 chunks per lane)
+    (6, 512, 64, 32, True),   # 1 expert per lane, top-32
+    (5, 256, 65, 8, True),    # 2 per lane with one expert in the second slice
+    (4, 256, 129, 1, False),  # 4 per lane, top-1
+    (9, 1024, 200, 32, False),
 ])
 def test_router_bitexact_other_shapes(device, T, H, E, K, renorm):
     _router_case(device, T, H, E, K, renorm, 21)
