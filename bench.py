@@ -65,10 +65,24 @@ def parse_args():
     p.add_argument("--tree-nodes", type=int, default=60)
     p.add_argument("--tree-depth", type=int, default=6)
     p.add_argument("--verify-slots", type=int, default=12)
+    p.add_argument("--executor", choices=("layer", "ready_demand", "predicted"), default="layer",
+                   help="48-layer forwards only. layer: each MoE layer's own resident-first, "
+                        "one-ahead sequence; ready_demand: the predicted-prefetch scheduler "
+                        "(Qwen3ExpertPrefetch) with no predictions, the reference's measured "
+                        "decode executor; predicted (cold48 only): the scheduler given each "
+                        "forward's own routed experts as predictions (captured in an untimed run "
+                        "of the same forward: an upper bound for a draft's predictions)")
+    p.add_argument("--max-inflight", type=int, default=2,
+                   help="the scheduler's bound on incomplete transfers (default 2, the "
+                        "reference's default)")
     p.add_argument("--record", choices=("full", "k3", "none"), default="full",
                    help="timing events of the recorded pass: K3 launches + one copy window "
                         "per step (full), K3 only, or none (no recorded pass)")
     args = p.parse_args()
+    if args.executor != "layer" and args.workload not in ("verify48", "cold48"):
+        p.error("--executor applies to the 48-layer forwards (verify48, cold48)")
+    if args.executor == "predicted" and args.workload != "cold48":
+        p.error("--executor predicted needs cold48 (its capture run would warm verify48's caches)")
     if args.steps is None:
         args.steps = 10 if args.workload in ("verify48", "cold48") else 50
     return args
@@ -202,9 +216,39 @@ def main_verify(args) -> int:
     seeds = [torch.randint(config.vocab_size, (1, 1), generator=g).to(dev) for _ in range(n)]
 
     cold = args.workload == "cold48"
+    executor = args.executor
+    predictions = [{} for _ in range(n)]
+    if executor == "predicted":
+        # Each forward's routed experts per layer, from the routers' outputs
+        # (the triple's indices, as the reference's route capture reads
+        # them) in an untimed run of the same forward from empty caches.
+        routed = [set() for _ in target.model.layers]
+        hooks = [layer.mlp.gate.register_forward_hook(
+                     lambda mod, inp, out, ids=ids: ids.update(out[2].flatten().tolist()))
+                 for layer, ids in zip(target.model.layers, routed)]
+        try:
+            with torch.inference_mode():
+                for i in range(n):
+                    for ids in routed:
+                        ids.clear()
+                    loaded.cold_reset_expert_caches()
+                    verify_draft_tree(target, trees[i], seeds[i], cache, commit=False)
+                    cache.crop(args.context)
+                    predictions[i] = {l: tuple(sorted(ids)) for l, ids in enumerate(routed)}
+        finally:
+            for h in hooks:
+                h.remove()
+        log(f"captured the routed experts of {n} forwards")
+    sched_stats = []
 
     def step(i):
-        res = verify_draft_tree(target, trees[i], seeds[i], cache, commit=False)
+        if executor == "layer":
+            res = verify_draft_tree(target, trees[i], seeds[i], cache, commit=False)
+        else:
+            with loaded.prefetch_experts(predictions[i], lookahead_layers=1,
+                                         max_inflight=args.max_inflight) as sched:
+                res = verify_draft_tree(target, trees[i], seeds[i], cache, commit=False)
+            sched_stats.append(sched.stats())
         cache.crop(args.context)
         return res
 
@@ -283,7 +327,8 @@ def main_verify(args) -> int:
                    "layers": args.layers, "context": args.context, "tree_nodes": args.tree_nodes,
                    "tree_depth": args.tree_depth, "cache_slots": args.verify_slots,
                    "attention": "HIP tree attention (K5)",
-                   "execution_policy": "resident_first", "h2d_prefetch": True},
+                   "execution_policy": "resident_first", "h2d_prefetch": True,
+                   "executor": executor},
         "per_layer_tokens_per_s": value * args.layers,
         "roofline": {"bound": "hbm", "achieved": k3_achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": k3_achieved / HBM_PEAK_GBS, "traffic": None,
@@ -299,6 +344,19 @@ def main_verify(args) -> int:
                   "hits_per_layer": hits / (args.steps * args.layers)},
         "accepted_per_step": accepted / args.steps,
     }
+    if sched_stats:  # the timed pass's forwards
+        timed = sched_stats[args.warmup:args.warmup + args.steps]
+        rows = [row for st in timed for row in st["layers"]]
+        line["scheduler"] = {
+            "lookahead_layers": 1, "max_inflight": args.max_inflight,
+            "complete": all(st["complete"] for st in timed),
+            "peak_inflight": max(st["peak_inflight"] for st in timed),
+            "queue_capacity_waits": sum(st["queue_capacity_waits"] for st in timed) / len(timed),
+            "per_forward": {k: sum(r[k] for r in rows) / len(timed)
+                            for k in ("predicted_experts", "actual_experts", "ready_at_router",
+                                      "inflight_at_router", "missing_at_router",
+                                      "prediction_copies", "demand_copies",
+                                      "unused_prediction_copies", "compute_waits")}}
     print(json.dumps(line), flush=True)
     loaded.close()
     return 0
@@ -628,7 +686,8 @@ def main() -> int:
                                 f"prewarm {args.prewarm} cycles"),
                    "tokens": T, "hidden": H, "experts": E, "top_k": K, "intermediate": I,
                    "cache_slots": slots, "prewarm_cycles": args.prewarm,
-                   "execution_policy": "resident_first", "h2d_prefetch": True},
+                   "execution_policy": "resident_first", "h2d_prefetch": True,
+                   "executor": executor},
         "record": args.record,
         "recorded_ms_per_step": rec_wall / args.steps * 1e3 if rec_wall else None,
         "device_ms_per_step": step_stats(step_events),

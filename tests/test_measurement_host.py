@@ -160,3 +160,16 @@ def test_bench_refuses_more_than_one_gpu():
     out = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
                          capture_output=True, text=True, timeout=60, cwd=root)
     assert out.returncode == 2 and "one GPU only" in out.stderr and not out.stdout.strip()
+
+
+@pytest.mark.parametrize("argv,ok", [(["--executor", "ready_demand"], False),
+                                     (["--workload", "verify48", "--executor", "predicted"], False),
+                                     (["--workload", "verify48", "--executor", "ready_demand"], True),
+                                     (["--workload", "cold48", "--executor", "predicted"], True)])
+def test_bench_executor_applies_to_the_48_layer_forwards(monkeypatch, argv, ok):
+    monkeypatch.setattr(sys, "argv", ["bench.py", *argv])
+    if ok:
+        assert bench.parse_args().executor == argv[-1]
+    else:
+        with pytest.raises(SystemExit):
+            bench.parse_args()
