@@ -686,8 +686,7 @@ def main() -> int:
                                 f"prewarm {args.prewarm} cycles"),
                    "tokens": T, "hidden": H, "experts": E, "top_k": K, "intermediate": I,
                    "cache_slots": slots, "prewarm_cycles": args.prewarm,
-                   "execution_policy": "resident_first", "h2d_prefetch": True,
-                   "executor": executor},
+                   "execution_policy": "resident_first", "h2d_prefetch": True},
         "record": args.record,
         "recorded_ms_per_step": rec_wall / args.steps * 1e3 if rec_wall else None,
         "device_ms_per_step": step_stats(step_events),

@@ -37,3 +37,30 @@ def test_bench_prints_one_contract_line(device):
     assert d["device_ms_per_step"]["n"] == 2
     assert d["h2d"]["link_peak_gbs"] > 0 and 0 <= d["overlap"] <= 1
 
+
+
+@pytest.mark.parametrize("workload,executor", [("cold48", "predicted"), ("verify48", "ready_demand")])
+def test_bench_48_layer_forward_under_the_prefetch_scheduler(device, workload, executor):
+    """The 48-layer workloads under the reference's executor, shrunk to 2
+    layers, an 8-node tree and a 64-token context: one contract line whose
+    scheduler statistics show complete forwards (and, with predictions,
+    every routed expert predicted)."""
+    cmd = [sys.executable, "-u", os.path.join(ROOT, "bench.py"), "--workload", workload,
+           "--executor", executor, "--layers", "2", "--tree-nodes", "8", "--context", "64",
+           "--steps", "2", "--warmup", "1", "--record", "none"]
+    print("bench scheduler run:", " ".join(cmd[2:]), flush=True)
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=110, cwd=ROOT)
+    assert out.returncode == 0, out.stderr[-3000:]
+    lines = [line for line in out.stdout.splitlines() if line.strip()]
+    assert len(lines) == 1, out.stdout[-2000:]
+    d = json.loads(lines[0])
+    assert d["value"] > 0 and d["config"]["executor"] == executor and d["config"]["layers"] == 2
+    s = d["scheduler"]
+    assert s["complete"] and 1 <= s["peak_inflight"] <= s["max_inflight"] == 2
+    per = s["per_forward"]
+    assert per["actual_experts"] > 0
+    if executor == "predicted":
+        assert per["predicted_experts"] == per["actual_experts"]
+        assert per["unused_prediction_copies"] == 0
+    else:
+        assert per["predicted_experts"] == 0 and per["prediction_copies"] == 0
