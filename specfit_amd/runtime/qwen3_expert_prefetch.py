@@ -262,6 +262,11 @@ class Qwen3ExpertPrefetch:
         """Lease ``key``: resident/in-flight only, non-blocking, or (force) a
         demand acquisition that may queue a wait on a busy slot."""
         cache = self._caches[key.layer_id]
+        if resident_only and key not in cache._resident and key not in cache._inflight:
+            # The cache's resident-only probe returns None for such a key
+            # (publishing completed transfers only moves keys from in-flight
+            # to resident), so skip the call and its lock.
+            return False
         before = cache._submission_sequence
         if force:
             lease = cache._prefetch(key)
