@@ -1,5 +1,10 @@
-"""Immutable, validated cache snapshots
-(src/specfit/runtime/cache_snapshot.py:21-144)."""
+"""Immutable, validated cache snapshots.
+
+Interface of src/specfit/runtime/cache_snapshot.py:21-144: the three frozen
+records, their fields, and the error type and message of every invariant.
+The invariants are kept as rule tables (``_checks.Rule``), evaluated in
+table order by ``__post_init__``.
+"""
 from __future__ import annotations
 
 from dataclasses import dataclass
@@ -7,15 +12,19 @@ from typing import Hashable
 
 import torch
 
+from ._checks import Rule, count_rules, enforce
 from .lease import ExpertCacheStats
 
 
-def _nonnegative_ints(**values) -> None:
-    for name, value in values.items():
-        if isinstance(value, bool) or not isinstance(value, int):
-            raise TypeError(f"{name} must be an integer")
-        if value < 0:
-            raise ValueError(f"{name} must be non-negative")
+def _empty_slot_is_idle(s) -> bool:
+    return s.expert_id is not None or not (s.ready or s.active_leases or s.pending_use_guards)
+
+
+_SLOT_RULES = count_rules("slot_id", "generation", "active_leases", "last_used_sequence",
+                          "pending_use_guards") + (
+    Rule(lambda s: isinstance(s.ready, bool), TypeError, "ready must be a boolean"),
+    Rule(_empty_slot_is_idle, ValueError, "an empty slot cannot be ready or in use"),
+)
 
 
 @dataclass(frozen=True, slots=True)
@@ -29,15 +38,13 @@ class CacheSlotSnapshot:
     pending_use_guards: int
 
     def __post_init__(self) -> None:
-        _nonnegative_ints(slot_id=self.slot_id, generation=self.generation,
-                          active_leases=self.active_leases,
-                          last_used_sequence=self.last_used_sequence,
-                          pending_use_guards=self.pending_use_guards)
-        if not isinstance(self.ready, bool):
-            raise TypeError("ready must be a boolean")
-        if self.expert_id is None and (self.ready or self.active_leases
-                                       or self.pending_use_guards):
-            raise ValueError("an empty slot cannot be ready or in use")
+        enforce(self, _SLOT_RULES)
+
+
+_TRANSFER_RULES = count_rules("slot_id", "generation", "submission_sequence") + (
+    Rule(lambda t: isinstance(t.ready_event_completed, bool), TypeError,
+         "ready_event_completed must be a boolean"),
+)
 
 
 @dataclass(frozen=True, slots=True)
@@ -50,10 +57,51 @@ class PendingTransferSnapshot:
     ready_event_completed: bool
 
     def __post_init__(self) -> None:
-        _nonnegative_ints(slot_id=self.slot_id, generation=self.generation,
-                          submission_sequence=self.submission_sequence)
-        if not isinstance(self.ready_event_completed, bool):
-            raise TypeError("ready_event_completed must be a boolean")
+        enforce(self, _TRANSFER_RULES)
+
+
+def _pending_sequences(snap) -> list[int]:
+    return [t.submission_sequence for t in snap.pending_transfers]
+
+
+def _assignments_unique(snap) -> bool:
+    held = [s.expert_id for s in snap.slots if s.expert_id is not None]
+    return len(held) == len(set(held))
+
+
+def _transfer_slots(snap):
+    """(transfer, its slot or None) for every pending transfer."""
+    by_slot = {s.slot_id: s for s in snap.slots}
+    return [(t, by_slot.get(t.slot_id)) for t in snap.pending_transfers]
+
+
+_SNAPSHOT_RULES = (
+    Rule(lambda g: bool(g.cache_id) and bool(g.queue_id), ValueError,
+         "cache_id and queue_id must be non-empty"),
+    *count_rules("capacity", "host_state_version", "lru_sequence", "submission_sequence"),
+    Rule(lambda g: g.capacity != 0, ValueError, "cache capacity must be positive"),
+    Rule(lambda g: isinstance(g.slots, tuple), TypeError, "slots must be an immutable tuple"),
+    Rule(lambda g: isinstance(g.pending_transfers, tuple), TypeError,
+         "pending_transfers must be an immutable tuple"),
+    Rule(lambda g: len(g.slots) == g.capacity, ValueError,
+         "snapshot must contain every cache slot"),
+    Rule(lambda g: [s.slot_id for s in g.slots] == list(range(g.capacity)), ValueError,
+         "slot IDs must cover range(capacity)"),
+    Rule(_assignments_unique, ValueError, "current expert assignments must be unique"),
+    Rule(lambda g: _pending_sequences(g) == sorted(_pending_sequences(g)), ValueError,
+         "pending transfers must follow submission order"),
+    Rule(lambda g: len(set(_pending_sequences(g))) == len(g.pending_transfers), ValueError,
+         "pending submission sequences must be unique"),
+    Rule(lambda g: all(q < g.submission_sequence for q in _pending_sequences(g)), ValueError,
+         "pending sequence must precede the submission counter"),
+    Rule(lambda g: all(slot is not None for _, slot in _transfer_slots(g)), ValueError,
+         "pending transfer references an unknown slot"),
+    Rule(lambda g: all(t.generation <= slot.generation for t, slot in _transfer_slots(g)),
+         ValueError, "pending transfer generation exceeds its current slot"),
+    Rule(lambda g: all(t.generation != slot.generation or t.expert_id == slot.expert_id
+                       for t, slot in _transfer_slots(g)),
+         ValueError, "current pending transfer does not match its slot"),
+)
 
 
 @dataclass(frozen=True, slots=True)
@@ -69,37 +117,4 @@ class GpuExpertCacheSnapshot:
     stats: ExpertCacheStats
 
     def __post_init__(self) -> None:
-        if not self.cache_id or not self.queue_id:
-            raise ValueError("cache_id and queue_id must be non-empty")
-        _nonnegative_ints(capacity=self.capacity, host_state_version=self.host_state_version,
-                          lru_sequence=self.lru_sequence,
-                          submission_sequence=self.submission_sequence)
-        if self.capacity == 0:
-            raise ValueError("cache capacity must be positive")
-        if not isinstance(self.slots, tuple):
-            raise TypeError("slots must be an immutable tuple")
-        if not isinstance(self.pending_transfers, tuple):
-            raise TypeError("pending_transfers must be an immutable tuple")
-        if len(self.slots) != self.capacity:
-            raise ValueError("snapshot must contain every cache slot")
-        if tuple(s.slot_id for s in self.slots) != tuple(range(self.capacity)):
-            raise ValueError("slot IDs must cover range(capacity)")
-        assigned = [s.expert_id for s in self.slots if s.expert_id is not None]
-        if len(assigned) != len(set(assigned)):
-            raise ValueError("current expert assignments must be unique")
-        seqs = [t.submission_sequence for t in self.pending_transfers]
-        if seqs != sorted(seqs):
-            raise ValueError("pending transfers must follow submission order")
-        if len(seqs) != len(set(seqs)):
-            raise ValueError("pending submission sequences must be unique")
-        if any(q >= self.submission_sequence for q in seqs):
-            raise ValueError("pending sequence must precede the submission counter")
-        by_id = {s.slot_id: s for s in self.slots}
-        for t in self.pending_transfers:
-            slot = by_id.get(t.slot_id)
-            if slot is None:
-                raise ValueError("pending transfer references an unknown slot")
-            if t.generation > slot.generation:
-                raise ValueError("pending transfer generation exceeds its current slot")
-            if t.generation == slot.generation and t.expert_id != slot.expert_id:
-                raise ValueError("current pending transfer does not match its slot")
+        enforce(self, _SNAPSHOT_RULES)

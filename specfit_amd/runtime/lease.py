@@ -1,10 +1,24 @@
-"""Expert leases and cache counters (src/specfit/runtime/lease.py:13-105).
+"""Expert leases and cache counters.
 
-A lease pins one *generation* of one cache slot: while any lease is active
-the slot is never chosen as an eviction victim.  ``wait(stream)`` orders the
-stream after the slot's H2D ready event and returns the packed weights;
-``release()`` records a use event on every stream that consumed the weights,
-so a later overwrite of the slot waits for those readers.
+Interface of src/specfit/runtime/lease.py:13-105: ``NoEvictableSlotError``,
+the frozen ``ExpertCacheStats`` record and ``ExpertLease`` (context manager,
+``wait(stream=None) -> Tensor``, idempotent ``release()``, ``slot_id``,
+``ready_event``).
+
+A lease is a handle on one *generation* of one cache slot.  Its life is a
+three-state machine:
+
+    OPEN --wait()--> OPEN (stream recorded as a reader)
+    OPEN --release()--> CLOSED                 (guards recorded, pin dropped)
+    OPEN --_release_keep_pinned()--> PINNED --_unpin()--> CLOSED
+
+PINNED exists for the batched layer forward: the release bookkeeping (LRU
+touch, observer event) happens at the reference's point in the lease
+sequence, while the pin that keeps the slot from being chosen as a victim
+stays until the kernel that reads the slot has been enqueued; ``_unpin``
+then records that kernel's stream as the slot's use guard.  All policy
+state (pins, touches, guards, observer events) lives in the cache; the
+lease only carries its identity, its readers and its state.
 """
 from __future__ import annotations
 
@@ -30,31 +44,35 @@ class ExpertCacheStats:
     pending_use_guards: int
 
 
+_OPEN, _PINNED, _CLOSED = 0, 1, 2
+
+
 class ExpertLease:
-    """Context manager over one leased slot generation."""
+    """One leased slot generation (see the module docstring)."""
 
-    __slots__ = ("_cache", "_expert_id", "_generation", "_released", "_streams",
-                 "_touch_on_wait", "_ready_known", "_unpin_pending", "ready_event", "slot_id")
+    __slots__ = ("_cache", "_key", "_generation", "_state", "_readers", "_touch_pending",
+                 "_ready_known", "ready_event", "slot_id")
 
-    def __init__(self, cache: "GpuExpertCache", expert_id: Hashable, slot_id: int,
-                 generation: int, ready_event: torch.cuda.Event, *,
-                 _defer_touch: bool = False) -> None:
+    def __init__(self, cache: "GpuExpertCache", key: Hashable, slot_id: int, generation: int,
+                 ready_event: torch.cuda.Event, *, touch_pending: bool = False,
+                 ready_known: bool = False) -> None:
         self._cache = cache
-        self._expert_id = expert_id
+        self._key = key
         self._generation = generation
-        self._released = False
-        self._streams: dict[int, torch.cuda.Stream] = {}
-        self._touch_on_wait = _defer_touch
-        # Set only when the ready event is already known to be complete; the
-        # lease still protects this generation.
-        self._ready_known = False
-        self._unpin_pending = False
+        self._state = _OPEN
+        # Streams that consumed the weights: {raw stream handle: Stream}.
+        self._readers: dict[int, torch.cuda.Stream] = {}
+        # A prefetch lease defers its LRU touch to its first wait.
+        self._touch_pending = touch_pending
+        # True when the ready event is known complete (a resident hit): the
+        # wait then queues no stream dependency.
+        self._ready_known = ready_known
         self.slot_id = slot_id
         self.ready_event = ready_event
 
     @property
     def expert_id(self) -> Hashable:
-        return self._expert_id
+        return self._key
 
     @property
     def generation(self) -> int:
@@ -62,56 +80,45 @@ class ExpertLease:
 
     @property
     def released(self) -> bool:
-        return self._released
+        return self._state != _OPEN
 
     def wait(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-        """Order ``stream`` (default: current) after the slot's H2D and return
-        the slot's packed weights."""
-        if self._released:
+        """Make ``stream`` (default: the current stream) wait for the slot's
+        H2D transfer and return the slot's packed weights."""
+        if self._state != _OPEN:
             raise RuntimeError("cannot wait on a released expert lease")
+        cache = self._cache
         if stream is None:
-            stream = torch.cuda.current_stream(self._cache.device)
+            stream = torch.cuda.current_stream(cache.device)
         if not self._ready_known:
             stream.wait_event(self.ready_event)
-        self._streams[int(stream.cuda_stream)] = stream
-        weights = self._cache._lease_tensor(self._expert_id, self.slot_id, self._generation,
-                                            touch=self._touch_on_wait)
-        self._touch_on_wait = False
-        if self._cache._observer is not None:
-            self._cache._record_consume_wait(expert_id=self._expert_id, slot_id=self.slot_id,
-                                             generation=self._generation,
-                                             ready_event=self.ready_event, stream=stream)
-        return weights
+        self._readers[int(stream.cuda_stream)] = stream
+        return cache._consume(self, stream)
 
     def release(self) -> None:
-        """Idempotent: record use guards on the consuming streams and unpin."""
-        if self._released:
-            return
-        self._cache._release(self._expert_id, self.slot_id, self._generation,
-                             tuple(self._streams.values()))
-        self._released = True
+        """Record use guards on the consuming streams and drop the pin.
+        Idempotent."""
+        if self._state == _OPEN:
+            self._cache._finish(self, keep_pin=False)
+            self._state = _CLOSED
 
     def _release_keep_pinned(self) -> None:
-        """Do the release bookkeeping now (LRU touch, observer event) but keep
-        the slot pinned until ``_unpin`` -- used when the kernel that reads the
-        weights is enqueued after this point in host order."""
-        if self._released:
-            return
-        self._cache._release(self._expert_id, self.slot_id, self._generation,
-                             tuple(self._streams.values()), keep_pinned=True)
-        self._released = True
-        self._unpin_pending = True
+        """Release bookkeeping now; the pin (and the guard) when ``_unpin``."""
+        if self._state == _OPEN:
+            self._cache._finish(self, keep_pin=True)
+            self._state = _PINNED
 
     def _unpin(self) -> None:
-        """Record the use guards and drop the pin taken by _release_keep_pinned."""
-        if not self._unpin_pending:
-            return
-        self._unpin_pending = False
-        self._cache._unpin(self._expert_id, self.slot_id, self._generation,
-                           tuple(self._streams.values()))
+        if self._state == _PINNED:
+            self._cache._unpin_many((self,))
+
+    # The pin protocol shared with the cache's run pins: the slots this pin
+    # holds, as (slot id, key, generation) triples.
+    def _pinned_slots(self):
+        return ((self.slot_id, self._key, self._generation),)
 
     def __enter__(self) -> "ExpertLease":
-        if self._released:
+        if self._state != _OPEN:
             raise RuntimeError("cannot re-enter a released expert lease")
         return self
 

@@ -1,31 +1,54 @@
 """Predicted expert prefetch for exactly one target forward.
 
-Drop-in for src/specfit/runtime/qwen3_expert_prefetch.py:34-418
-(``Qwen3ExpertPrefetch``): the executor every measured decode of the
-reference runs under (with ``predictions={}`` it is the "ready_demand"
-executor).  Policy, all host-side:
+Interface of src/specfit/runtime/qwen3_expert_prefetch.py:34-418
+(``Qwen3ExpertPrefetch``: constructor arguments and their errors, context
+protocol, ``experts(layer, active)``, ``stats()``, ``events()``), the
+executor every measured decode of the reference runs under
+(run_specfit_main_comparison.py:552-555; with ``predictions={}`` it is the
+"ready_demand" executor).
 
-* every layer cache's copies go to one shared copy stream; at most
-  ``max_inflight`` new transfers are incomplete at a time;
-* the current layer's demand is served before future predictions; while a
-  layer has no routes yet, speculation keeps at least one slot of it free
-  for demand (``max_prefetch_per_layer`` can lower that limit further);
-* predicted experts that are already resident are protected once per layer
-  before any earlier-id miss could evict them;
-* when a layer's router has run, wrong predictions are dropped and the
-  actual experts are yielded ready-first (transfer complete), else the
-  oldest in-flight, else a free queue credit is awaited or a demand copy is
-  forced into a busy slot (the only case that queues a use-guard wait);
-* streams, hooks and leases are restored on exit, including on exceptions.
+Policy (the reference's):
 
-GPU work is ordered with events; the only host waits are the queue-credit
-``Event.synchronize`` of the reference.
+* every layer cache's copies go to one shared copy stream, and at most
+  ``max_inflight`` transfers (including ones still running from before the
+  context) are incomplete at a time;
+* the current layer's demand is placed before future layers' predictions;
+  a layer without routes yet may hold at most ``slot_count - 1`` experts
+  (``max_prefetch_per_layer`` can lower that), so one slot stays free for
+  demand; with ``lookahead_layers`` = n, predictions of the n layers after
+  the current one are placed too;
+* predicted experts that are already resident are protected (held) once
+  per layer, before any earlier-id miss could evict them;
+* once a layer's router has run, wrong predictions are dropped and actual
+  experts are handed out completed-transfer first (ascending id), else the
+  oldest held one in flight (the layer's kernel waits for it on the GPU),
+  else one queue credit is awaited or a demand copy is forced into a busy
+  slot (the only case that may queue a use-guard wait);
+* with ``eviction_policy="probability"``, a speculative copy only replaces
+  a writable victim of strictly lower predicted probability.
+
+How this build runs it (MI355X host path):
+
+* The shared copy stream completes transfers in submission order, so the
+  scheduler tracks its own transfers as a FIFO of holds and learns which
+  are complete by querying only the oldest incomplete one: no per-expert
+  event polling, and a hold becomes "ready" exactly once.
+* Ready experts of the routed layer are collected in a set as their
+  transfers complete; ``expert_batches`` hands the layer every ready expert
+  at once (ascending id), which the layer computes with ONE grouped K3
+  launch and releases together (one use-guard event for the batch).
+  ``experts`` keeps the reference's one-expert-at-a-time protocol.
+* Each layer's queue, holdings and counters live in a ``_LayerPlan``.
+
+Batches change when leases are released relative to the scheduler's own
+decisions (a batch's leases are released together, after its launch), not
+what is computed: outputs are bitwise those of the per-layer path.
 """
 from __future__ import annotations
 
 import math
 from collections import deque
-from contextlib import ExitStack
+from contextlib import ExitStack, closing
 from dataclasses import asdict, dataclass
 from numbers import Real
 from typing import Mapping, Sequence
@@ -52,8 +75,72 @@ class _LayerStats:
     compute_waits: int = 0
 
 
-def _is_int(value) -> bool:
-    return type(value) is int
+# Ways the scheduler asks a cache for an expert.
+_RESIDENT_ONLY = 0   # join an in-flight transfer or hit a resident slot, else nothing
+_SPECULATE = 1       # non-blocking copy of a predicted expert
+_DEMAND = 2          # non-blocking copy of a routed expert
+_FORCE = 3           # routed expert into a busy slot (may queue a use-guard wait)
+
+
+class _Hold:
+    """A lease the scheduler holds for one expert."""
+
+    __slots__ = ("key", "lease", "rank", "ready")
+
+    def __init__(self, key: ExpertKey, lease: ExpertLease, rank: tuple, ready: bool) -> None:
+        self.key = key
+        self.lease = lease
+        # Order of "oldest in flight": joined transfers (-1, cache sequence)
+        # before the scheduler's own copies (0, copy number).
+        self.rank = rank
+        self.ready = ready
+
+
+class _LayerPlan:
+    """Requests, holdings and counters of one decoder layer."""
+
+    __slots__ = ("layer", "cache", "limit", "keys", "requests", "held", "routed", "protected",
+                 "scores", "stats", "prediction_copies")
+
+    def __init__(self, layer: int, cache, limit: int, keys: dict, predicted: tuple,
+                 scores: dict | None) -> None:
+        self.layer = layer
+        self.cache = cache
+        self.limit = limit
+        self.keys = keys                      # expert id -> the cache's key object
+        self.requests = deque(keys[e] for e in predicted)
+        self.held = 0                         # holds of this layer
+        self.routed: set | None = None        # actual experts, once the router ran
+        self.protected = False                # predicted residents held once
+        self.scores = scores                  # key -> probability (probability eviction)
+        self.stats = _LayerStats(layer, len(predicted))
+        self.prediction_copies: set[int] = set()
+
+    def key(self, expert: int) -> ExpertKey:
+        k = self.keys.get(expert)
+        return k if k is not None else ExpertKey(self.layer, expert)
+
+
+def _natural(value, minimum: int) -> bool:
+    return type(value) is int and value >= minimum
+
+
+def _layer_keys(cache, layer: int) -> dict:
+    return {k.expert_id: k for k in cache._sources
+            if type(k) is ExpertKey and k.layer_id == layer}
+
+
+def _checked_scores(supplied, keys: dict, layer: int) -> dict[int, float]:
+    if not isinstance(supplied, Mapping):
+        raise TypeError("each probability layer must map expert IDs to probabilities")
+    scores = {}
+    for expert, value in supplied.items():
+        if (type(expert) is not int or expert not in keys or type(value) is bool
+                or not isinstance(value, Real) or not math.isfinite(value)
+                or not 0 <= value <= 1):
+            raise ValueError(f"invalid expert probability in layer {layer}")
+        scores[expert] = float(value)
+    return scores
 
 
 class Qwen3ExpertPrefetch:
@@ -64,12 +151,11 @@ class Qwen3ExpertPrefetch:
                  max_prefetch_per_layer: int | None = None, trace: bool = False,
                  prediction_probabilities: Mapping[int, Mapping[int, float]] | None = None,
                  eviction_policy: str = "lru") -> None:
-        if not _is_int(lookahead_layers) or lookahead_layers < 0:
+        if not _natural(lookahead_layers, 0):
             raise ValueError("lookahead_layers must be an integer >= 0")
-        if not _is_int(max_inflight) or max_inflight < 1:
+        if not _natural(max_inflight, 1):
             raise ValueError("max_inflight must be an integer >= 1")
-        if max_prefetch_per_layer is not None and (
-                not _is_int(max_prefetch_per_layer) or max_prefetch_per_layer < 0):
+        if max_prefetch_per_layer is not None and not _natural(max_prefetch_per_layer, 0):
             raise ValueError("max_prefetch_per_layer must be a non-negative integer or None")
         if type(trace) is not bool:
             raise ValueError("trace must be a boolean")
@@ -77,97 +163,79 @@ class Qwen3ExpertPrefetch:
             raise TypeError("predictions must map layer IDs to expert IDs")
         if eviction_policy not in ("lru", "probability"):
             raise ValueError("eviction_policy must be 'lru' or 'probability'")
-        if prediction_probabilities is None and eviction_policy != "lru":
+        scored = prediction_probabilities is not None
+        if not scored and eviction_policy != "lru":
             raise ValueError("probability eviction requires prediction_probabilities")
-        if prediction_probabilities is not None and not isinstance(prediction_probabilities, Mapping):
+        if scored and not isinstance(prediction_probabilities, Mapping):
             raise TypeError("prediction_probabilities must map layers to expert probabilities")
-        self._loaded = loaded
         self._layers = tuple(loaded.model.model.layers)
-        self._caches = tuple(loaded.expert_caches)
-        n_layers = len(self._layers)
-        if not self._layers or n_layers != len(self._caches):
+        caches = tuple(loaded.expert_caches)
+        n = len(self._layers)
+        if not n or n != len(caches):
             raise ValueError("decoder layers and expert caches must match")
-        for name, mapping in (("prediction", predictions),
+        for what, mapping in (("prediction", predictions),
                               ("probability", prediction_probabilities or {})):
-            if any(not _is_int(layer) or not 0 <= layer < n_layers for layer in mapping):
-                raise ValueError(f"{name} layer is outside the loaded model")
-        # Speculation may hold at most slots-1 slots of a layer.
-        self._limits = tuple(
-            min(len(c._slots) - 1, len(c._slots) - 1 if max_prefetch_per_layer is None
-                else max_prefetch_per_layer)
-            for c in self._caches)
-        self._probabilities: list[dict | None] = []
-        self._requests: list[deque] = []
-        normalized = []
-        for layer, cache in enumerate(self._caches):
-            ids = tuple(predictions.get(layer, ()))
-            keys = {}
-            if ids or prediction_probabilities is not None:
-                keys = {k.expert_id: k for k in cache._sources
-                        if type(k) is ExpertKey and k.layer_id == layer}
-            if any(not _is_int(e) or e not in keys for e in ids):
-                raise ValueError(f"invalid predicted expert in layer {layer}")
-            probs = None
-            if prediction_probabilities is not None:
-                supplied = prediction_probabilities.get(layer, {})
-                if not isinstance(supplied, Mapping):
-                    raise TypeError("each probability layer must map expert IDs to probabilities")
-                scores: dict[int, float] = {}
-                probs = {}
-                for expert, value in supplied.items():
-                    if (not _is_int(expert) or expert not in keys or type(value) is bool
-                            or not isinstance(value, Real) or not math.isfinite(value)
-                            or not 0 <= value <= 1):
-                        raise ValueError(f"invalid expert probability in layer {layer}")
-                    scores[expert] = float(value)
-                    probs[keys[expert]] = float(value)
-                if any(e not in scores for e in ids):
+            if not all(type(lid) is int and 0 <= lid < n for lid in mapping):
+                raise ValueError(f"{what} layer is outside the loaded model")
+        plans, normalized = [], []
+        for lid, cache in enumerate(caches):
+            slots = len(cache._slots)
+            limit = slots - 1 if max_prefetch_per_layer is None else min(
+                slots - 1, max_prefetch_per_layer)
+            wanted = tuple(predictions.get(lid, ()))
+            keys = _layer_keys(cache, lid)
+            if not all(type(e) is int and e in keys for e in wanted):
+                raise ValueError(f"invalid predicted expert in layer {lid}")
+            scores = None
+            if scored:
+                given = _checked_scores(prediction_probabilities.get(lid, {}), keys, lid)
+                if not all(e in given for e in wanted):
                     raise ValueError("every predicted expert needs an explicit probability")
-                ids = tuple(sorted((e for e in set(ids) if scores[e] > 0),
-                                   key=lambda e: (-scores[e], e)))[: self._limits[layer]]
+                # Highest probability first (ties: lower id), zero dropped,
+                # at most the layer's speculation limit.
+                ranked = sorted((e for e in set(wanted) if given[e] > 0),
+                                key=lambda e: (-given[e], e))
+                wanted = tuple(ranked[:limit])
+                scores = {keys[e]: p for e, p in given.items()}
             else:
-                ids = tuple(sorted(set(ids)))
-            self._probabilities.append(probs)
-            normalized.append(ids)
-            self._requests.append(deque(keys[e] for e in ids))
-        if len({c.device for c in self._caches}) != 1:
+                wanted = tuple(sorted(set(wanted)))
+            normalized.append(wanted)
+            plans.append(_LayerPlan(lid, cache, limit, keys, wanted, scores))
+        if len({c.device for c in caches}) != 1:
             raise ValueError("prefetch requires all layers on one GPU")
         self.predictions = tuple(normalized)
         self.lookahead_layers = lookahead_layers
         self.max_inflight = max_inflight
         self.eviction_policy = eviction_policy
+        self._caches = caches
+        self._plans = plans
         self._trace = trace
-        self._events: list[dict] = []
+        self._log: list[dict] = []
         self._stack = ExitStack()
-        self._leases: dict[ExpertKey, ExpertLease] = {}
-        self._held_counts = [0] * n_layers
-        self._speculative_leases = 0
-        self._ranks: dict[ExpertKey, tuple[int, int]] = {}
-        self._pending: list[torch.cuda.Event] = []
-        # A transfer's event never becomes incomplete again, so once seen
-        # complete it is remembered (bounds event queries).
-        self._ready_events: set = set()
-        self._prediction_copies: set[ExpertKey] = set()
-        self._prediction_residents_checked: set[int] = set()
-        self._actual: dict[int, set[int]] = {}
-        self._layer_stats = [_LayerStats(i, len(ids)) for i, ids in enumerate(self.predictions)]
-        self._copy_sequence = 0
+        self._holds: dict[ExpertKey, _Hold] = {}
+        self._copies: deque[_Hold] = deque()   # own transfers not yet seen complete, in order
+        self._prior: list[torch.cuda.Event] = []  # incomplete transfers from before entry
+        self._joined: list[_Hold] = []          # holds that joined a transfer not ours
+        self._copy_count = 0
+        self._speculative = 0
+        self._routed_layer: int | None = None   # layer whose experts are being handed out
+        self._remaining: dict[int, ExpertKey] = {}
+        self._ready_ids: set[int] = set()
         self._next_layer = 0
         self._open_layer: int | None = None
-        self._current_layer = 0
+        self._current = 0
         self._entered = self._used = self._complete = False
-        self._peak_inflight = self._peak_speculative_leases = 0
-        self._queue_capacity_waits = self._slot_wait_copies = 0
+        self._peak_inflight = self._peak_speculative = 0
+        self._capacity_waits = self._slot_wait_copies = 0
 
-    # ------------------------------------------------------------ context --
+    # -------------------------------------------------------------- context --
     def __enter__(self) -> "Qwen3ExpertPrefetch":
         if self._used:
             raise RuntimeError("a prefetch context cannot be reused")
         modules = tuple(layer.mlp.experts for layer in self._layers)
-        for layer, (module, cache) in enumerate(zip(modules, self._caches)):
-            if (not isinstance(module, Qwen3OffloadedExperts) or module.cache is not cache
-                    or module.layer_id != layer):
-                raise RuntimeError("every decoder layer must contain its offloaded expert cache")
+        if not all(isinstance(m, Qwen3OffloadedExperts) and m.cache is c and m.layer_id == lid
+                   for lid, (m, c) in enumerate(zip(modules, self._caches))):
+            raise RuntimeError("every decoder layer must contain its offloaded expert cache")
         if any(m.reduction_mode is not ReductionMode.CANONICAL for m in modules):
             raise ValueError("predicted prefetch requires canonical reduction")
         if any(m._prediction_scheduler is not None for m in modules):
@@ -176,41 +244,40 @@ class Qwen3ExpertPrefetch:
             raise RuntimeError("prefetch requires open caches without active leases")
         self._used = True
         try:
-            self._copy_stream = torch.cuda.Stream(device=self._caches[0].device)
+            stream = torch.cuda.Stream(device=self._caches[0].device)
+            self._copy_stream = stream
             for cache in self._caches:
-                original = cache.copy_stream
-                self._copy_stream.wait_stream(original)
-                if cache._aux_copy_stream is not original:
-                    self._copy_stream.wait_stream(cache._aux_copy_stream)
-                # Earlier incomplete transfers keep consuming queue credits.
-                self._pending.extend(t.ready_event for t in cache._outstanding_transfers
-                                     if not t.ready_event.query())
-                cache.copy_stream = self._copy_stream
-                self._stack.callback(self._restore_stream, cache, original)
+                own = cache.copy_stream
+                for earlier in {id(own): own, id(cache._aux_copy_stream): cache._aux_copy_stream
+                                }.values():
+                    stream.wait_stream(earlier)
+                # Transfers still running keep their queue credits.
+                self._prior += [t.ready_event for t in cache._outstanding_transfers
+                                if not t.ready_event.query()]
+                cache.copy_stream = stream
+                self._stack.callback(self._give_back_stream, cache, own)
             for lid, (layer, module) in enumerate(zip(self._layers, modules)):
                 module._prediction_scheduler = self
                 self._stack.callback(setattr, module, "_prediction_scheduler", None)
-                handle = layer.self_attn.register_forward_pre_hook(self._attention_hook(lid))
-                self._stack.callback(handle.remove)
+                hook = layer.self_attn.register_forward_pre_hook(self._attention_hook(lid))
+                self._stack.callback(hook.remove)
             self._entered = True
-            self._record("prediction_available")
+            self._note("prediction_available")
             self._pump()
             return self
         except BaseException:
-            for key in tuple(self._leases):
-                self._take_lease(key).release()
+            self._release_all()
             self._entered = False
             self._stack.close()
             raise
 
-    def _restore_stream(self, cache, original) -> None:
-        original.wait_stream(self._copy_stream)
-        cache.copy_stream = original
+    def _give_back_stream(self, cache, own) -> None:
+        own.wait_stream(self._copy_stream)
+        cache.copy_stream = own
 
     def __exit__(self, exc_type, exc, tb) -> None:
         try:
-            for key in tuple(self._leases):
-                self._take_lease(key).release()
+            self._release_all()
         finally:
             self._entered = False
             self._stack.close()
@@ -218,207 +285,282 @@ class Qwen3ExpertPrefetch:
         if exc_type is None and not self._complete:
             raise RuntimeError("prefetch context requires exactly one complete target forward")
 
-    # ------------------------------------------------------------ helpers --
-    def _record(self, action, *, layer=None, expert=None, **values) -> None:
+    def _release_all(self) -> None:
+        for key in tuple(self._holds):
+            self._drop(key).release()
+
+    # ---------------------------------------------------------------- trace --
+    def _note(self, action, *, layer=None, expert=None, **values) -> None:
         if self._trace:
-            self._events.append(dict(sequence=len(self._events), action=action,
-                                     current_layer=self._current_layer, layer_id=layer,
-                                     expert_id=expert, **values))
+            self._log.append(dict(sequence=len(self._log), action=action,
+                                  current_layer=self._current, layer_id=layer,
+                                  expert_id=expert, **values))
 
     def _attention_hook(self, layer: int):
         def hook(module, inputs):
-            del module, inputs
             self._begin_layer(layer)
         return hook
 
     def _begin_layer(self, layer: int) -> None:
         if not self._entered or self._open_layer is not None or layer != self._next_layer:
             raise RuntimeError("predicted prefetch requires one ordered eager layer traversal")
-        self._current_layer = self._open_layer = layer
-        self._record("attention", layer=layer)
+        self._current = self._open_layer = layer
+        self._note("attention", layer=layer)
         self._pump()
 
-    def _event_ready(self, event) -> bool:
-        if event in self._ready_events:
-            return True
-        if event.query():
-            self._ready_events.add(event)
-            return True
-        return False
+    # ------------------------------------------------------------- holdings --
+    def _in_flight(self) -> int:
+        return len(self._prior) + len(self._copies)
 
-    def _reap(self) -> None:
-        self._pending = [e for e in self._pending if not self._event_ready(e)]
+    def _mark_ready(self, hold: _Hold) -> None:
+        hold.ready = True
+        key = hold.key
+        if key.layer_id == self._routed_layer and key.expert_id in self._remaining:
+            self._ready_ids.add(key.expert_id)
 
-    def _take_lease(self, key: ExpertKey) -> ExpertLease:
-        lease = self._leases.pop(key)
-        self._ranks.pop(key, None)
-        self._held_counts[key.layer_id] -= 1
-        if key.layer_id not in self._actual:
-            self._speculative_leases -= 1
-        return lease
+    def _advance(self) -> None:
+        """Learn which transfers completed: own copies in order (one query
+        for the oldest incomplete one, then the next...), then the few
+        transfers from before the context and joined ones."""
+        copies = self._copies
+        while copies and copies[0].lease.ready_event.query():
+            self._mark_ready(copies.popleft())
+        if self._prior:
+            self._prior = [ev for ev in self._prior if not ev.query()]
+        if self._joined:
+            waiting = []
+            for hold in self._joined:
+                if self._holds.get(hold.key) is not hold:
+                    continue
+                if hold.lease.ready_event.query():
+                    self._mark_ready(hold)
+                else:
+                    waiting.append(hold)
+            self._joined = waiting
 
-    def _hold(self, key: ExpertKey, *, resident_only: bool = False, force: bool = False,
-              prediction: bool = False) -> bool:
-        """Lease ``key``: resident/in-flight only, non-blocking, or (force) a
-        demand acquisition that may queue a wait on a busy slot."""
-        cache = self._caches[key.layer_id]
-        if resident_only and key not in cache._resident and key not in cache._inflight:
-            # The cache's resident-only probe returns None for such a key
-            # (publishing completed transfers only moves keys from in-flight
-            # to resident), so skip the call and its lock.
-            return False
+    def _hold(self, key: ExpertKey, mode: int) -> _Hold | None:
+        plan = self._plans[key.layer_id]
+        cache = plan.cache
+        if (mode == _RESIDENT_ONLY and key not in cache._resident and key not in cache._inflight
+                and key in cache._sources and not cache._closed):
+            # The resident-only lookup of such a key returns None (reaping
+            # moves keys from in flight to resident only); an unknown key or
+            # a closed cache still goes to the cache, which raises.
+            return None
         before = cache._submission_sequence
-        if force:
+        if mode == _FORCE:
             lease = cache._prefetch(key)
-        elif prediction and self.eviction_policy == "probability":
-            lease = cache._prefetch_nonblocking(
-                key, resident_only=resident_only,
-                eviction_probabilities=self._probabilities[key.layer_id])
+        elif mode == _SPECULATE and self.eviction_policy == "probability":
+            lease = cache._prefetch_nonblocking(key, eviction_probabilities=plan.scores)
         else:
-            lease = cache._prefetch_nonblocking(key, resident_only=resident_only)
+            lease = cache._prefetch_nonblocking(key, resident_only=mode == _RESIDENT_ONLY)
         if lease is None:
-            return False
-        self._leases[key] = lease
-        self._held_counts[key.layer_id] += 1
-        if key.layer_id not in self._actual:
-            self._speculative_leases += 1
-        if key in cache._resident:  # published only after its transfer completed
-            self._ready_events.add(lease.ready_event)
-        if cache._submission_sequence != before:
-            self._pending.append(lease.ready_event)
-            self._ranks[key] = (0, self._copy_sequence)
-            self._copy_sequence += 1
-            stats = self._layer_stats[key.layer_id]
-            if prediction:
-                self._prediction_copies.add(key)
-                stats.prediction_copies += 1
+            return None
+        plan.held += 1
+        if plan.routed is None:
+            self._speculative += 1
+            self._peak_speculative = max(self._peak_speculative, self._speculative)
+        if cache._submission_sequence != before:  # this call copied the expert
+            hold = _Hold(key, lease, (0, self._copy_count), False)
+            self._copy_count += 1
+            self._copies.append(hold)
+            self._peak_inflight = max(self._peak_inflight, self._in_flight())
+            if mode == _SPECULATE:
+                plan.stats.prediction_copies += 1
+                plan.prediction_copies.add(key.expert_id)
             else:
-                stats.demand_copies += 1
-            self._peak_inflight = max(self._peak_inflight, len(self._pending))
-            self._record("copy", layer=key.layer_id, expert=key.expert_id,
-                         prediction=prediction, slot_wait=force)
+                plan.stats.demand_copies += 1
+            self._note("copy", layer=key.layer_id, expert=key.expert_id,
+                       prediction=mode == _SPECULATE, slot_wait=mode == _FORCE)
+        elif key in cache._resident:  # residency is published after completion
+            hold = _Hold(key, lease, (-1, -1), True)
         else:
             transfer = cache._inflight.get(key)
-            self._ranks[key] = (-1, transfer.submission_sequence if transfer else -1)
-        self._peak_speculative_leases = max(self._peak_speculative_leases,
-                                            self._speculative_leases)
+            hold = _Hold(key, lease, (-1, transfer.submission_sequence if transfer else -1), False)
+            self._joined.append(hold)
+        self._holds[key] = hold
+        if hold.ready:
+            self._mark_ready(hold)
+        return hold
+
+    def _drop(self, key: ExpertKey) -> ExpertLease:
+        hold = self._holds.pop(key)
+        plan = self._plans[key.layer_id]
+        plan.held -= 1
+        if plan.routed is None:
+            self._speculative -= 1
+        return hold.lease
+
+    # ------------------------------------------------------------ placement --
+    def _pump(self) -> None:
+        """Place requests nearest layer first within the queue credits and
+        the per-layer speculation limits; a layer that cannot place its
+        next request stops placement for the layers after it."""
+        self._advance()
+        stop = min(len(self._plans), self._current + self.lookahead_layers + 1)
+        for plan in self._plans[self._current:stop]:
+            if not self._place(plan):
+                return
+
+    def _place(self, plan: _LayerPlan) -> bool:
+        demand = plan.routed is not None
+        holds = self._holds
+        if not demand and not plan.protected:
+            plan.protected = True
+            cache = plan.cache
+            if cache._resident or cache._inflight:
+                for key in plan.requests:
+                    if plan.held >= plan.limit:
+                        break
+                    if key not in holds:
+                        self._hold(key, _RESIDENT_ONLY)
+        queue = plan.requests
+        mode = _DEMAND if demand else _SPECULATE
+        while queue:
+            key = queue[0]
+            if key not in holds:
+                if not demand and plan.held >= plan.limit:
+                    return False
+                if self._hold(key, _RESIDENT_ONLY) is None:
+                    if self._in_flight() >= self.max_inflight or self._hold(key, mode) is None:
+                        return False
+            queue.popleft()
         return True
 
-    def _pump(self) -> None:
-        """Place requests, nearest layer first, within the queue and slot
-        limits."""
-        self._reap()
-        last = min(len(self._layers), self._current_layer + self.lookahead_layers + 1)
-        for layer in range(self._current_layer, last):
-            demand = layer in self._actual
-            if not demand and layer not in self._prediction_residents_checked:
-                cache = self._caches[layer]
-                if cache._resident or cache._inflight:
-                    for key in self._requests[layer]:
-                        if self._held_counts[layer] >= self._limits[layer]:
-                            break
-                        if key not in self._leases:
-                            self._hold(key, resident_only=True)
-                self._prediction_residents_checked.add(layer)
-            requests = self._requests[layer]
-            while requests:
-                key = requests[0]
-                if key in self._leases:
-                    requests.popleft()
-                    continue
-                if not demand and self._held_counts[layer] >= self._limits[layer]:
-                    return
-                if self._hold(key, resident_only=True):
-                    requests.popleft()
-                    continue
-                if len(self._pending) >= self.max_inflight:
-                    return
-                if not self._hold(key, prediction=not demand):
-                    return
-                requests.popleft()
-
-    # ---------------------------------------------------------- execution --
-    def experts(self, layer: int, active_experts: tuple[int, ...]):
-        """Yield each actual expert of ``layer`` once, completed transfers
-        first; the yielded lease is released when the generator resumes."""
-        if not self._entered or self._open_layer != layer or layer in self._actual:
+    # ------------------------------------------------------------ execution --
+    def _route(self, layer: int, active_experts) -> _LayerPlan:
+        """The router of ``layer`` ran: drop wrong predictions, hold the
+        actual residents, count what is ready, queue the rest as demand."""
+        if not self._entered or self._open_layer != layer or self._plans[layer].routed is not None:
             raise RuntimeError("expert scheduling must follow this layer's Attention exactly once")
+        plan = self._plans[layer]
         actual = set(active_experts)
-        self._speculative_leases -= self._held_counts[layer]
-        self._actual[layer] = actual
-        remaining = dict.fromkeys(ExpertKey(layer, e) for e in sorted(actual))
-        stats = self._layer_stats[layer]
+        self._speculative -= plan.held
+        plan.routed = actual
+        stats = plan.stats
         stats.actual_experts = len(actual)
-        self._record("router", layer=layer, experts=list(active_experts))
-        for key in tuple(self._leases):
-            if key.layer_id == layer and key.expert_id not in actual:
-                self._take_lease(key).release()
-        stats.unused_prediction_copies = sum(k.layer_id == layer and k.expert_id not in actual
-                                             for k in self._prediction_copies)
-        for key in remaining:
-            if key not in self._leases:
-                self._hold(key, resident_only=True)
-            lease = self._leases.get(key)
-            if lease is None:
+        self._note("router", layer=layer, experts=list(active_experts))
+        for key in [k for k in self._holds if k.layer_id == layer and k.expert_id not in actual]:
+            self._drop(key).release()
+        stats.unused_prediction_copies = len(plan.prediction_copies - actual)
+        self._advance()
+        self._routed_layer = layer
+        self._remaining = remaining = {e: plan.key(e) for e in sorted(actual)}
+        self._ready_ids = set()
+        for e, key in remaining.items():
+            hold = self._holds.get(key) or self._hold(key, _RESIDENT_ONLY)
+            if hold is None:
                 stats.missing_at_router += 1
-            elif self._event_ready(lease.ready_event):
+            elif hold.ready:
                 stats.ready_at_router += 1
+                self._ready_ids.add(e)
             else:
                 stats.inflight_at_router += 1
-        self._requests[layer] = deque(k for k in remaining if k not in self._leases)
-        while remaining:
-            self._pump()
-            ready = oldest = None
-            for candidate in remaining:
-                lease = self._leases.get(candidate)
-                if lease is None:
-                    continue
-                if self._event_ready(lease.ready_event):
-                    ready = candidate
-                    break
-                if oldest is None or self._ranks[candidate] < self._ranks[oldest]:
-                    oldest = candidate
-            if ready is not None:
-                key, waited = ready, False
-            elif oldest is not None:
-                key, waited = oldest, True
-                stats.compute_waits += 1
-            else:
-                self._reap()
-                if len(self._pending) >= self.max_inflight:
-                    # Only earlier or speculative transfers are in flight and
-                    # nothing can run: free one queue credit.
-                    self._queue_capacity_waits += 1
-                    self._pending[0].synchronize()
-                    continue
-                # Every reusable slot may still be read by submitted kernels:
-                # only this demand fallback queues a use-guard wait.
-                key = next(iter(remaining))
-                self._hold(key, force=True)
-                self._slot_wait_copies += 1
-                continue
-            lease = self._take_lease(key)
-            del remaining[key]
-            self._record("compute", layer=layer, expert=key.expert_id, waited=waited)
-            try:
-                yield key.expert_id, lease
-                stats.computed_experts += 1
-            finally:
-                lease.release()
+        plan.requests = deque(k for k in remaining.values() if k not in self._holds)
+        return plan
+
+    def _oldest_in_flight(self) -> _Hold | None:
+        """The held, not yet ready routed expert with the smallest rank."""
+        remaining, layer = self._remaining, self._routed_layer
+        best = None
+        for hold in self._joined:
+            k = hold.key
+            if (k.layer_id == layer and k.expert_id in remaining and not hold.ready
+                    and self._holds.get(k) is hold and (best is None or hold.rank < best.rank)):
+                best = hold
+        if best is not None:
+            return best
+        for hold in self._copies:
+            k = hold.key
+            if k.layer_id == layer and k.expert_id in remaining and self._holds.get(k) is hold:
+                return hold
+        return None
+
+    def _steps(self, layer: int, active_experts, batched: bool):
+        """Core of ``experts`` / ``expert_batches``: yields lists of
+        (expert id, lease); the leases are released when it resumes."""
+        plan = self._route(layer, active_experts)
+        stats = plan.stats
+        remaining = self._remaining
+        try:
+            while remaining:
+                self._pump()
+                ready = self._ready_ids
+                if ready:
+                    ids = sorted(ready) if batched else [min(ready)]
+                    ready.difference_update(ids)
+                    waited = False
+                else:
+                    hold = self._oldest_in_flight()
+                    if hold is None:
+                        if self._in_flight() >= self.max_inflight:
+                            # Only speculative or earlier transfers are in
+                            # flight and nothing routed can run: free a credit.
+                            self._capacity_waits += 1
+                            first = self._prior[0] if self._prior else self._copies[0].lease.ready_event
+                            first.synchronize()
+                            continue
+                        # Every writable slot is taken: the one demand copy
+                        # allowed to queue a wait on a busy slot.
+                        self._hold(next(iter(remaining.values())), _FORCE)
+                        self._slot_wait_copies += 1
+                        continue
+                    ids = [hold.key.expert_id]
+                    waited = True
+                    stats.compute_waits += 1
+                keys = [remaining.pop(e) for e in ids]
+                leases = [self._drop(k) for k in keys]
+                for e in ids:
+                    self._note("compute", layer=layer, expert=e, waited=waited)
+                try:
+                    yield list(zip(ids, leases))
+                    stats.computed_experts += len(ids)
+                finally:
+                    self._release_batch(plan.cache, leases)
+        finally:
+            self._routed_layer = None
+            self._ready_ids = set()
         self._pump()
         self._open_layer = None
         self._next_layer = layer + 1
-        self._record("layer_complete", layer=layer)
+        self._note("layer_complete", layer=layer)
+
+    @staticmethod
+    def _release_batch(cache, leases: list) -> None:
+        """Release a batch whose weights one launch read: per-lease release
+        bookkeeping, then one use-guard event per reader stream."""
+        if len(leases) == 1:
+            leases[0].release()
+            return
+        for lease in leases:
+            lease._release_keep_pinned()
+        cache._unpin_many(leases)
+
+    def expert_batches(self, layer: int, active_experts: tuple[int, ...]):
+        """Yield the actual experts of ``layer`` in batches: every expert
+        whose transfer has completed (ascending id), else the oldest in
+        flight alone.  A batch's leases are released when the generator
+        resumes, so the caller enqueues the batch's kernel before that."""
+        return self._steps(layer, active_experts, True)
+
+    def experts(self, layer: int, active_experts: tuple[int, ...]):
+        """Yield each actual expert of ``layer`` once, completed transfers
+        first; the yielded lease is released when the generator resumes."""
+        steps = self._steps(layer, active_experts, False)
+        with closing(steps):
+            for batch in steps:
+                yield batch[0]
 
     def stats(self) -> dict:
         """Host-side statistics (no GPU synchronisation)."""
         return dict(complete=self._complete, lookahead_layers=self.lookahead_layers,
-                    max_inflight=self.max_inflight, prefetch_slot_limits=list(self._limits),
+                    max_inflight=self.max_inflight,
+                    prefetch_slot_limits=[p.limit for p in self._plans],
                     peak_inflight=self._peak_inflight,
-                    peak_speculative_leases=self._peak_speculative_leases,
-                    queue_capacity_waits=self._queue_capacity_waits,
+                    peak_speculative_leases=self._peak_speculative,
+                    queue_capacity_waits=self._capacity_waits,
                     slot_wait_copies=self._slot_wait_copies,
-                    layers=[asdict(row) for row in self._layer_stats])
+                    layers=[asdict(p.stats) for p in self._plans])
 
     def events(self) -> tuple[dict, ...]:
-        return tuple(dict(row) for row in self._events)
+        return tuple(dict(row) for row in self._log)

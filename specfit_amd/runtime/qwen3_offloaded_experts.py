@@ -198,20 +198,23 @@ class Qwen3OffloadedExperts(nn.Module):
 
     def _forward_slot_table(self, hidden_states, top_k_index, top_k_weights):
         """Resident-first forward whose resident experts start before the
-        routes reach the host: right after K2 and the counts read it starts,
-        one K3 launch over the device slot table (the slot of every expert
-        whose copy has completed or is in flight; the launch waits for the
-        latter) computes every such expert that has rows while the host
-        waits for the counts.  Then the reference lease sequence runs unchanged
-        (resident hits, one-ahead prefetch, misses), with K3 launches only
-        for the experts the table launch did not cover: misses, transfers
-        submitted after the table was taken, and experts with more rows than
-        tokens (repeated ids in a token's routes), whose rows the table
-        launch computed with the split of a smaller expert.  Holding the
-        cache lock from the table to the end of the sequence keeps every
-        table slot in place until its lease records the use guard that
-        covers the table launch (the lease is released on the compute
-        stream after it)."""
+        routes reach the host: right after K2, one K3 launch over the device
+        slot table (the slot of every expert whose transfer has completed,
+        -1 otherwise) computes every resident expert that has rows while
+        the host waits for the counts.  Then the reference lease sequence
+        runs unchanged (resident hits, one-ahead prefetch, misses), with K3
+        launches only for the experts the table launch did not cover:
+        misses, transfers still in flight when the table was taken, and
+        experts with more rows than tokens (repeated ids in a token's
+        routes), whose rows the table launch computed with the split of a
+        smaller expert.
+
+        Why no table slot is overwritten while the table launch reads it:
+        the launch reads only resident experts that have rows; in
+        resident-first order every one of them is leased (and its lease
+        records a use guard after the table launch on the compute stream)
+        before the first miss chooses a victim, and the cache lock is held
+        from the table to the end of the sequence."""
         T, K = top_k_index.shape
         if hidden_states.dtype != torch.bfloat16:
             raise ValueError("hidden_states must be bfloat16")
@@ -223,14 +226,11 @@ class Qwen3OffloadedExperts(nn.Module):
         with cache._lock:
             # Host work before K2, so the table launch follows the counts
             # read without a host gap.
-            version, slots, pending = cache._slot_table(self._keys)
+            version, slots = cache._slot_table(self._keys)
             table = self._upload_slot_table(version, slots, dev)
             routes = self._new_routes(hidden_states, top_k_weights, None)
-            stream = torch.cuda.current_stream(dev)
             plan = _dispatch(top_k_index, num_experts, self._counts_staging(num_experts))
             routes.plan = plan
-            for ready in pending:  # transfers still in flight
-                stream.wait_event(ready)
             entry = ops.grouped_swiglu_table(routes.hidden, plan, routes.route_weights, table,
                                              routes.storage, self.hidden_size,
                                              self.intermediate_size, routes.act, routes.rows,
@@ -254,18 +254,19 @@ class Qwen3OffloadedExperts(nn.Module):
         self._run_in_order(order, routes)
         self._last_forward_copied = self.cache._stats.h2d_submissions != before
 
-    def _upload_slot_table(self, version: int, slots: list[int],
+    def _upload_slot_table(self, version: int | None, slots: list[int],
                            device: torch.device) -> torch.Tensor:
         """Copy the slot table to the device on the current stream, unless
-        the table of this cache version is already there.  The pinned
-        staging is reused: the previous forward's upload was ordered before
-        its counts read, which that forward waited for."""
+        the table of this resident-map version is already there (``None``:
+        an unversioned map, always uploaded).  The pinned staging is reused:
+        the previous forward's upload was ordered before its counts read,
+        which that forward waited for."""
         E = len(slots)
         if self._table_host is None or self._table_host.numel() != E:
             self._table_host = torch.empty(E, dtype=torch.int32, pin_memory=True)
             self._table_dev = torch.empty(E, dtype=torch.int32, device=device)
             self._table_version = None
-        if version != self._table_version:
+        if version is None or version != self._table_version:
             self._table_host.numpy()[:] = slots
             self._table_dev.copy_(self._table_host, non_blocking=True)
             self._table_version = version
@@ -273,21 +274,22 @@ class Qwen3OffloadedExperts(nn.Module):
 
     def _forward_prefetched(self, hidden_states, top_k_index, top_k_weights):
         """Scheduler-driven forward (qwen3_offloaded_experts.py:166-203): the
-        scheduler yields leased experts in the order it chooses (ready
-        transfers first) and releases each lease when resumed, so every
-        yielded expert is launched before control returns to it.  Outputs
-        are reduced canonically."""
+        scheduler hands out leased experts in the order it chooses (completed
+        transfers first) in batches; each batch is computed by one grouped K3
+        launch, enqueued before control returns to the scheduler, which then
+        releases the batch's leases.  Outputs are reduced canonically."""
         routes, active = self._prepare(hidden_states, top_k_index, top_k_weights)
-        scheduled = self._prediction_scheduler.experts(self.layer_id, active)
+        scheduler = self._prediction_scheduler
+        batches = scheduler.expert_batches(self.layer_id, active)
         stream = torch.cuda.current_stream(self.cache.device)
-        with closing(scheduled):
-            for expert_id, lease in scheduled:
+        with closing(batches):
+            for batch in batches:
                 if routes is None:
                     raise RuntimeError("scheduler yielded an expert for an empty layer")
-                weights = lease.wait(stream)
-                routes.expert_ids = [expert_id]
+                routes.expert_ids = [e for e, _ in batch]
                 routes.tag = "scheduled"
-                _expert_forward(routes.hidden, [weights], hidden_size=self.hidden_size,
+                _expert_forward(routes.hidden, [lease.wait(stream) for _, lease in batch],
+                                hidden_size=self.hidden_size,
                                 intermediate_size=self.intermediate_size, routes=routes)
         if routes is None:
             return torch.zeros_like(hidden_states)
