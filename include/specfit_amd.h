@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 6
+#define SF_ABI_VERSION 7
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -54,6 +54,7 @@ extern "C" {
 #define SF_ERR_UNSUPPORTED_SHAPE 2
 #define SF_ERR_MISALIGNED 3
 #define SF_ERR_TOO_MANY_EXPERTS 4
+#define SF_ERR_SCRATCH_LIMIT 5
 #define SF_ERR_HIP_BASE 1000
 
 /* Largest expert count the router, dispatch and combine kernels accept. */
@@ -174,6 +175,35 @@ int sf_grouped_swiglu_table(const void *hidden, const int32_t *perm_pos,
                             const void *slot_base, int64_t slot_stride_elems,
                             void *act_workspace, void *out_rows,
                             sf_stream_t stream);
+
+/*
+ * K3, device slot-table form, allocating nothing.  No counterpart in the
+ * reference: this entry point is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, results and limits as
+ * sf_grouped_swiglu_table minus act_workspace: the [tokens * top_k,
+ * intermediate_size] bf16 activation workspace is taken from a fixed device
+ * array of SF_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds
+ * until the process ends.
+ * Limit: tokens * top_k * intermediate_size * 2 <= SF_NOALLOC_SCRATCH_BYTES
+ * (4 MiB: 341 tokens at top_k 8 and intermediate 768), else
+ * SF_ERR_SCRATCH_LIMIT and nothing is launched.
+ * Every call on one GPU shares that GPU's array, which keeps the last
+ * call's contents: calls that overlap on one GPU (kernels on concurrent
+ * streams, or host threads) race.  Nothing in it needs to start at zero:
+ * each activation row a launch reads is written first by the same launch.
+ */
+#define SF_NOALLOC_SCRATCH_BYTES (4u << 20)
+int sf_grouped_swiglu_table_noalloc(const void *hidden, const int32_t *perm_pos,
+                                    const int32_t *offsets,
+                                    const void *route_weights, int tokens,
+                                    int top_k, int hidden_size,
+                                    int intermediate_size, int num_experts,
+                                    int max_rows,
+                                    const int32_t *slot_of_expert,
+                                    const void *slot_base,
+                                    int64_t slot_stride_elems, void *out_rows,
+                                    sf_stream_t stream);
 
 /*
  * K3 on already-gathered rows of one expert (the _expert_forward seam,

@@ -10,7 +10,7 @@ import threading
 
 from .build import LIB_PATH
 
-SF_ABI_VERSION = 6
+SF_ABI_VERSION = 7
 SF_ERR_HIP_BASE = 1000
 
 _lock = threading.Lock()
@@ -29,6 +29,8 @@ SIGNATURES = {
     "sf_dispatch": ([_p, _i, _i, _i, _p, _p, _p, _p, _p, _p], _i),
     "sf_grouped_swiglu": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p], _i),
     "sf_grouped_swiglu_table": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _p, _p, _p], _i),
+    "sf_grouped_swiglu_table_noalloc": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _p,
+                                         _p], _i),
     "sf_expert_swiglu": ([_p, _i, _i64, _i, _i, _p, _p, _p, _p], _i),
     "sf_combine": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p], _i),
     "sf_copy_h2d": ([_p, _p, _sz, _p], _i),

@@ -15,6 +15,8 @@ extern "C" const char* sf_error_string(int code) {
       return "misaligned buffer";
     case SF_ERR_TOO_MANY_EXPERTS:
       return "too many experts";
+    case SF_ERR_SCRATCH_LIMIT:
+      return "workspace exceeds the allocation-free entry point's scratch array";
     default:
       break;
   }

@@ -43,6 +43,8 @@
 // row: an MFMA output row depends only on its own A row and such rows are
 // never stored, so loads need no per-lane branches.
 // MFMA: v_mfma_f32_16x16x32_bf16, A = token rows (M), B = weight rows (N).
+#include <mutex>
+
 #include "sf_common.h"
 
 namespace {
@@ -707,22 +709,16 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
   return SF_OK;
 }
 
-extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_pos,
-                                       const int32_t* offsets, const void* route_weights,
-                                       int tokens, int top_k, int hidden_size,
-                                       int intermediate_size, int num_experts, int max_rows,
-                                       const int32_t* slot_of_expert,
-                                       const void* slot_base, int64_t slot_stride_elems,
-                                       void* act_workspace, void* out_rows,
-                                       sf_stream_t stream) {
-  int rc = check_common(tokens, top_k, hidden_size, intermediate_size);
-  if (rc) return rc;
-  if (num_experts < 1 || slot_stride_elems < 0 || max_rows < 1) return SF_ERR_INVALID_ARGUMENT;
-  if (tokens == 0) return SF_OK;
-  if (!hidden || !perm_pos || !offsets || !slot_of_expert || !slot_base ||
-      !act_workspace || !out_rows)
-    return SF_ERR_INVALID_ARGUMENT;
-  const bool aligned = aligned16(hidden) && aligned16(act_workspace) && aligned16(slot_base) &&
+namespace {
+
+// Slot-table launch shared by sf_grouped_swiglu_table and its
+// allocation-free variant; `act` is the activation workspace.
+int table_launch(const void* hidden, const int32_t* perm_pos, const int32_t* offsets,
+                 const void* route_weights, int tokens, int top_k, int hidden_size,
+                 int intermediate_size, int num_experts, int max_rows,
+                 const int32_t* slot_of_expert, const void* slot_base,
+                 int64_t slot_stride_elems, void* act, void* out_rows, hipStream_t stream) {
+  const bool aligned = aligned16(hidden) && aligned16(act) && aligned16(slot_base) &&
                        (slot_stride_elems % 8 == 0);
   const Shape shape = aligned ? mfma_shape(hidden_size, intermediate_size) : Shape::kGeneric;
   SwigluArgs a{};
@@ -730,7 +726,7 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
   a.perm_pos = perm_pos;
   a.offsets = offsets;
   a.route_w = static_cast<const uint16_t*>(route_weights);
-  a.act = static_cast<uint16_t*>(act_workspace);
+  a.act = static_cast<uint16_t*>(act);
   a.out = static_cast<uint16_t*>(out_rows);
   a.row_stride = hidden_size;
   a.top_k = top_k;
@@ -740,8 +736,109 @@ extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_p
   a.slot_of_expert = slot_of_expert;
   a.slot_base = static_cast<const uint16_t*>(slot_base);
   a.slot_stride = slot_stride_elems;
-  return launch<Resolve::kTable>(a, num_experts, shape, max_rows,
-                                 reinterpret_cast<hipStream_t>(stream));
+  return launch<Resolve::kTable>(a, num_experts, shape, max_rows, stream);
+}
+
+int check_table(int tokens, int top_k, int hidden_size, int intermediate_size, int num_experts,
+                int max_rows, int64_t slot_stride_elems) {
+  const int rc = check_common(tokens, top_k, hidden_size, intermediate_size);
+  if (rc) return rc;
+  if (num_experts < 1 || slot_stride_elems < 0 || max_rows < 1) return SF_ERR_INVALID_ARGUMENT;
+  return SF_OK;
+}
+
+// ------------------------------------------------ allocation-free variant --
+// The activation workspace of sf_grouped_swiglu_table_noalloc lives in this
+// fixed device array (one copy per GPU, held until the process ends).  Host
+// code never passes `scratch` itself to a kernel: in host code that name is
+// a host-side stand-in, so each device's address is looked up once with
+// hipGetSymbolAddress and used instead.
+constexpr size_t kScratchBytes = SF_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint16_t scratch[kScratchBytes / sizeof(uint16_t)];
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceScratch {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t status = hipSuccess;
+};
+
+DeviceScratch g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the device of `stream` (the current device
+// for the null stream), resolved on that device's first call with the device
+// made current for the lookup.
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  const hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return SF_ERR_HIP_BASE + static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return SF_ERR_INVALID_ARGUMENT;
+  DeviceScratch& ds = g_scratch[dev];
+  std::call_once(ds.once, [&] {
+    int current = -1;
+    hipError_t st = hipGetDevice(&current);
+    if (st == hipSuccess && current != dev) st = hipSetDevice(dev);
+    void* p = nullptr;
+    if (st == hipSuccess) st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (current >= 0 && current != dev) {
+      const hipError_t back = hipSetDevice(current);
+      if (st == hipSuccess) st = back;
+    }
+    ds.status = st;
+    ds.ptr = st == hipSuccess ? p : nullptr;
+  });
+  if (ds.status != hipSuccess) return SF_ERR_HIP_BASE + static_cast<int>(ds.status);
+  *out = ds.ptr;
+  return SF_OK;
+}
+
+}  // namespace
+
+extern "C" int sf_grouped_swiglu_table(const void* hidden, const int32_t* perm_pos,
+                                       const int32_t* offsets, const void* route_weights,
+                                       int tokens, int top_k, int hidden_size,
+                                       int intermediate_size, int num_experts, int max_rows,
+                                       const int32_t* slot_of_expert,
+                                       const void* slot_base, int64_t slot_stride_elems,
+                                       void* act_workspace, void* out_rows,
+                                       sf_stream_t stream) {
+  const int rc = check_table(tokens, top_k, hidden_size, intermediate_size, num_experts,
+                             max_rows, slot_stride_elems);
+  if (rc) return rc;
+  if (tokens == 0) return SF_OK;
+  if (!hidden || !perm_pos || !offsets || !slot_of_expert || !slot_base ||
+      !act_workspace || !out_rows)
+    return SF_ERR_INVALID_ARGUMENT;
+  return table_launch(hidden, perm_pos, offsets, route_weights, tokens, top_k, hidden_size,
+                      intermediate_size, num_experts, max_rows, slot_of_expert, slot_base,
+                      slot_stride_elems, act_workspace, out_rows,
+                      reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int sf_grouped_swiglu_table_noalloc(const void* hidden, const int32_t* perm_pos,
+                                               const int32_t* offsets, const void* route_weights,
+                                               int tokens, int top_k, int hidden_size,
+                                               int intermediate_size, int num_experts,
+                                               int max_rows, const int32_t* slot_of_expert,
+                                               const void* slot_base, int64_t slot_stride_elems,
+                                               void* out_rows, sf_stream_t stream) {
+  const int rc = check_table(tokens, top_k, hidden_size, intermediate_size, num_experts,
+                             max_rows, slot_stride_elems);
+  if (rc) return rc;
+  if (tokens == 0) return SF_OK;
+  if (!hidden || !perm_pos || !offsets || !slot_of_expert || !slot_base || !out_rows)
+    return SF_ERR_INVALID_ARGUMENT;
+  const size_t need = static_cast<size_t>(tokens) * static_cast<size_t>(top_k) *
+                      static_cast<size_t>(intermediate_size) * sizeof(uint16_t);
+  if (need > kScratchBytes) return SF_ERR_SCRATCH_LIMIT;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  void* act = nullptr;
+  const int sr = scratch_address(s, &act);
+  if (sr) return sr;
+  return table_launch(hidden, perm_pos, offsets, route_weights, tokens, top_k, hidden_size,
+                      intermediate_size, num_experts, max_rows, slot_of_expert, slot_base,
+                      slot_stride_elems, act, out_rows, s);
 }
 
 extern "C" int sf_expert_swiglu(const void* rows, int m, int64_t row_stride,

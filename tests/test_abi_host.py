@@ -37,10 +37,11 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_error_strings():
-    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 6
+    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 7
     assert _native.error_string(0) == "success"
     assert _native.error_string(1) == "invalid argument"
     assert _native.error_string(12345) != ""
+    assert "scratch" in _native.error_string(5)
     with pytest.raises(RuntimeError, match="invalid argument"):
         _native.check(1, "probe")
 
