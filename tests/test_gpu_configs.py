@@ -1,0 +1,265 @@
+"""Whole-layer parity at every benchmark configuration of the MoE block.
+
+Each test runs the drop-in runtime (router module -> Qwen3OffloadedExperts
+over a GpuExpertCache) on the configuration's real shapes and cache, then
+checks the routing bit-exact against the oracle's router and the MoE output
+against the oracle's fp32 layer (max |y - y32| / max |y32| <= 1e-2) and the
+bf16-eager layer (allclose rtol = atol = 1.6e-2), as the reference's
+offloaded-model test compares against HF eager
+(tests/gpu/test_qwen3_offloaded_model.py:154-272):
+
+* 16 tokens, all 128 experts resident in 128 slots, uniform routing: the
+  slot-table forward (asserted to be the path taken);
+* 64 tokens, 24-slot LRU cache, Zipf(1.1) routing after pre-warm cycles;
+* 1 / 8 / 32 / 64 / 128 tokens with a 12-slot cache, Zipf routing;
+* the 48-layer verification forward (60-node tree over a 1024-token
+  context, 12 slots per layer) and the cold 128-token forward (every cache
+  emptied first): forward hooks capture every layer's router input and
+  output and every MoE block's input and output; routing is checked on all
+  48 layers, the MoE output on four.
+"""
+from __future__ import annotations
+
+from unittest.mock import patch
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from specfit_amd import ops
+from specfit_amd.runtime import (ExpertKey, GpuExpertCache, Qwen3MoeTopKRouterHip,
+                                 Qwen3OffloadedExperts)
+from specfit_amd.workloads import make_hidden, make_layer
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K = 2048, 768, 128, 8
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+class _Fp32Experts(dict):
+    """expert id -> fp32 packed weights, converted from bf16 on first use."""
+
+    def __init__(self, packed: torch.Tensor) -> None:
+        super().__init__()
+        self._packed = packed
+
+    def __missing__(self, e: int) -> np.ndarray:
+        value = self[e] = oracle.bf16_float(_bits(self._packed[e]))
+        return value
+
+
+@pytest.fixture(scope="module")
+def uniform_layer():
+    layer = make_layer(seed=0, pin_memory=True)
+    return layer, _Fp32Experts(layer.experts)
+
+
+@pytest.fixture(scope="module")
+def zipf_layer():
+    layer = make_layer(seed=0, zipf_s=1.1, zipf_lambda=1.0, pin_memory=True)
+    return layer, _Fp32Experts(layer.experts)
+
+
+def _check_routing(hidden, router_weight, logits, w, idx, where: str):
+    o_logits, o_w, o_idx, _ = oracle.router(_bits(hidden), _bits(router_weight), K, True)
+    assert np.array_equal(_bits(logits), o_logits), f"{where}: logits differ from the oracle"
+    assert np.array_equal(idx.cpu().numpy(), o_idx), f"{where}: indices differ from the oracle"
+    assert np.array_equal(_bits(w), o_w), f"{where}: weights differ from the oracle"
+    return o_idx, o_w
+
+
+def _check_moe(hidden, idx, w_bits, out, experts32, where: str, *, bf16_check: bool = True):
+    x = oracle.bf16_float(_bits(hidden))
+    wf = oracle.bf16_float(w_bits)
+    y32 = oracle.moe_forward_fp32(x, idx, wf, experts32, H, I)
+    got = oracle.bf16_float(_bits(out))
+    err = float(np.abs(got - y32).max() / np.abs(y32).max())
+    print(f"{where}: MoE max normalised error vs fp32 oracle {err:.3e}", flush=True)
+    assert err <= 1e-2, f"{where}: error {err:.3e} above 1e-2"
+    if bf16_check:
+        yb = oracle.moe_forward_bf16(x, idx, wf, experts32, H, I, E, accumulate_fp32=True)
+        np.testing.assert_allclose(got, yb, rtol=1.6e-2, atol=1.6e-2, err_msg=where)
+    return err
+
+
+def _layer_modules(device, layer, slots: int):
+    router = Qwen3MoeTopKRouterHip(num_experts=E, hidden_size=H, top_k=K, norm_topk_prob=True,
+                                   device=device)
+    with torch.no_grad():
+        router.weight.copy_(layer.router)
+    cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(E)},
+                           slot_count=slots, device=device, adopt_pinned_sources=True)
+    experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H, intermediate_size=I,
+                                    execution_policy="resident_first", h2d_prefetch=True)
+    return router, cache, experts
+
+
+def test_c1_resident16_slot_table_layer(device, uniform_layer):
+    layer, experts32 = uniform_layer
+    router, cache, experts = _layer_modules(device, layer, slots=E)
+    try:
+        for e in range(E):  # every expert resident
+            with cache.acquire(ExpertKey(0, e)) as lease:
+                lease.wait()
+        torch.cuda.synchronize()
+        assert len(cache.resident_expert_ids()) == E
+        h = make_hidden(16, seed=0).to(device)
+        logits, w, idx = router(h)
+        first = experts(h, idx, w)  # per-launch path (no earlier forward)
+        calls = []
+        real = ops.grouped_swiglu_table
+
+        def spy(*args, **kwargs):
+            calls.append(1)
+            return real(*args, **kwargs)
+
+        with patch.object(ops, "grouped_swiglu_table", spy):
+            before = cache.stats().h2d_submissions
+            second = experts(h, idx, w)
+        torch.cuda.synchronize()
+        assert calls == [1], "the all-resident layer did not take the slot-table forward"
+        assert cache.stats().h2d_submissions == before
+        assert torch.equal(first, second)
+        o_idx, o_w = _check_routing(h, layer.router, logits, w, idx, "C1")
+        _check_moe(h, o_idx, o_w, second, experts32, "C1")
+    finally:
+        cache.close()
+
+
+def _prewarmed_forward(device, layer, *, tokens: int, slots: int, prewarm: int, seed0: int):
+    router, cache, experts = _layer_modules(device, layer, slots)
+    for i in range(prewarm):
+        h = make_hidden(tokens, seed=seed0 + i, zipf_fold=True).to(device)
+        _, w, idx = router(h)
+        experts(h, idx, w)
+    torch.cuda.synchronize()
+    before = cache.stats()
+    h = make_hidden(tokens, seed=seed0 + prewarm, zipf_fold=True).to(device)
+    logits, w, idx = router(h)
+    out = experts(h, idx, w)
+    torch.cuda.synchronize()
+    after = cache.stats()
+    assert cache.active_lease_count == 0
+    cache.close()
+    return h, logits, w, idx, out, after.h2d_submissions - before.h2d_submissions
+
+
+def test_c2_layer_64_tokens_24_slots_zipf(device, zipf_layer):
+    layer, experts32 = zipf_layer
+    h, logits, w, idx, out, misses = _prewarmed_forward(device, layer, tokens=64, slots=24,
+                                                        prewarm=4, seed0=1)
+    print(f"C2: {misses} misses in the measured forward", flush=True)
+    assert misses > 0  # the miss path (H2D + per-group launches) is exercised
+    o_idx, o_w = _check_routing(h, layer.router, logits, w, idx, "C2")
+    _check_moe(h, o_idx, o_w, out, experts32, "C2")
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 32, 64, 128])
+def test_c3_sweep_12_slots_zipf(device, zipf_layer, tokens):
+    layer, experts32 = zipf_layer
+    h, logits, w, idx, out, misses = _prewarmed_forward(device, layer, tokens=tokens, slots=12,
+                                                        prewarm=2, seed0=100 + tokens)
+    print(f"C3 T={tokens}: {misses} misses", flush=True)
+    o_idx, o_w = _check_routing(h, layer.router, logits, w, idx, f"C3 T={tokens}")
+    _check_moe(h, o_idx, o_w, out, experts32, f"C3 T={tokens}")
+
+
+# ------------------------------------------------------- 48-layer forwards --
+@pytest.fixture(scope="module")
+def verify_model(device, uniform_layer):
+    from specfit_amd.workloads import make_kv_context, make_verify_model
+
+    layer, experts32 = uniform_layer
+    loaded = make_verify_model(device=device, layers=48, slots_per_layer=12,
+                               experts=layer)
+    cache = make_kv_context(loaded.model.config, 1024, device=device, seed=1)
+    torch.cuda.synchronize()
+    yield loaded, cache, experts32
+    loaded.close()
+
+
+def _captured_forward(loaded, cache, tree, seed_token):
+    """One verification forward with every layer's gate and MoE block
+    captured: (gate inputs, gate outputs, MoE inputs, MoE outputs)."""
+    from specfit_amd.runtime import verify_draft_tree
+
+    layers = loaded.model.model.layers
+    gate_in, gate_out, moe_in, moe_out = {}, {}, {}, {}
+    hooks = []
+    for lid, layer in enumerate(layers):
+        def on_gate(mod, inp, out, lid=lid):
+            gate_in[lid] = inp[0].detach().clone()
+            gate_out[lid] = tuple(t.detach().clone() for t in out)
+
+        def on_moe(mod, inp, out, lid=lid):
+            moe_in[lid] = tuple(t.detach().clone() for t in inp)
+            moe_out[lid] = out.detach().clone()
+
+        hooks.append(layer.mlp.gate.register_forward_hook(on_gate))
+        hooks.append(layer.mlp.experts.register_forward_hook(on_moe))
+    try:
+        with torch.inference_mode():
+            res = verify_draft_tree(loaded.model, tree, seed_token, cache, commit=False)
+        torch.cuda.synchronize()
+    finally:
+        for hk in hooks:
+            hk.remove()
+    return res, gate_in, gate_out, moe_in, moe_out
+
+
+def _check_48_layers(loaded, captured, experts32, tokens: int, where: str):
+    _, gate_in, gate_out, moe_in, moe_out = captured
+    layers = loaded.model.model.layers
+    assert len(gate_out) == len(moe_out) == 48
+    for lid in range(48):
+        h = gate_in[lid]
+        assert h.shape == (tokens, H)
+        logits, w, idx = gate_out[lid]
+        _check_routing(h, layers[lid].mlp.gate.weight, logits, w, idx, f"{where} layer {lid}")
+        hid, m_idx, m_w = moe_in[lid]
+        assert torch.equal(m_idx, idx) and torch.equal(m_w, w)
+    errs = []
+    for lid in (0, 16, 32, 47):
+        hid, m_idx, m_w = moe_in[lid]
+        errs.append(_check_moe(hid, m_idx.cpu().numpy(), _bits(m_w), moe_out[lid], experts32,
+                               f"{where} layer {lid}", bf16_check=False))
+    return errs
+
+
+def test_c4_verify48_routing_every_layer_and_moe_outputs(device, verify_model):
+    from specfit_amd.runtime import synthetic_tree
+
+    loaded, cache, experts32 = verify_model
+    config = loaded.model.config
+    tree = synthetic_tree(60, 6, seed=100, vocab=config.vocab_size)
+    seed_token = torch.tensor([[17]], device=device)
+    before = sum(c.stats().h2d_submissions for c in loaded.expert_caches)
+    captured = _captured_forward(loaded, cache, tree, seed_token)
+    cache.crop(1024)
+    misses = sum(c.stats().h2d_submissions for c in loaded.expert_caches) - before
+    print(f"C4: {misses} misses over 48 layers", flush=True)
+    assert misses > 0
+    _check_48_layers(loaded, captured, experts32, 61, "C4")
+
+
+def test_c5_cold48_routing_every_layer_and_moe_outputs(device, verify_model):
+    from specfit_amd.runtime import synthetic_tree
+
+    loaded, cache, experts32 = verify_model
+    config = loaded.model.config
+    torch.cuda.synchronize()
+    loaded.cold_reset_expert_caches()
+    assert all(not c.resident_expert_ids() for c in loaded.expert_caches)
+    tree = synthetic_tree(127, 6, seed=200, vocab=config.vocab_size)
+    seed_token = torch.tensor([[23]], device=device)
+    captured = _captured_forward(loaded, cache, tree, seed_token)
+    cache.crop(1024)
+    misses = [c.stats().h2d_submissions for c in loaded.expert_caches]
+    print(f"C5: misses per layer min {min(misses)} max {max(misses)}", flush=True)
+    assert min(misses) >= 100  # nearly every expert of every layer copied in
+    _check_48_layers(loaded, captured, experts32, 128, "C5")

@@ -112,3 +112,51 @@ def test_router_against_transformers_golden(name):
         assert np.all(np.abs(np.sort(got_w) - np.sort(hf_w)) <= np.abs(hf_w).max() * 2.0 ** -7)
     print(f"{name}: {exact_rows.sum()} rows with bitwise-equal logits, "
           f"{boundary_ties // 2} top-k boundary ties resolved differently by torch.topk")
+
+
+REAL_SHAPE = [("router_hf_t256_h2048_e128_k8_uniform.npz", None),
+              ("router_hf_t256_h2048_e128_k8_zipf.npz", 1.1)]
+
+
+def real_shape_case(name):
+    """(fixture, hidden bits, router bits) of a Qwen3-30B-A3B-shaped router
+    fixture; its inputs are regenerated and checked against the stored
+    digest first."""
+    import sys
+
+    sys.path.insert(0, GOLDEN)
+    import inputs
+
+    f = np.load(os.path.join(GOLDEN, name))
+    zipf = float(f["zipf_s"])
+    hidden, weight = inputs.real_shape_inputs(int(f["tokens"]), 2048, 128, int(f["seed"]),
+                                              None if zipf < 0 else zipf)
+    assert inputs.input_digest(hidden, weight) == str(f["input_sha256"]), \
+        "regenerated router inputs differ from the ones the fixture was made from"
+    return f, inputs.bits(hidden), inputs.bits(weight)
+
+
+@pytest.mark.parametrize("name,zipf", REAL_SHAPE)
+def test_router_agreement_with_transformers_at_the_qwen3_shape(name, zipf):
+    """H 2048, E 128, top-8 renormalised, 256 tokens: logits within one
+    bf16 ulp of transformers', and every expert-set difference is a tie at
+    the 8th logit (rows with equal logits) or a one-ulp flip at the
+    boundary."""
+    from _router_agreement import classify
+
+    f, h, w = real_shape_case(name)
+    logits, tw, ti, _ = oracle.router(h, w, 8, True)
+    a = classify(logits, ti, f["logits"], f["index"], 8)
+    print(f"{name}: {a.rows} rows, {a.exact_logit_rows} with bitwise-equal logits, "
+          f"{a.same_set_rows} same expert set ({a.agreement:.2%}); differences: "
+          f"{a.tie_rows} ties at the 8th logit, {a.flip_set_rows} one-ulp flips "
+          f"({a.flip_rows} rows with a flipped logit)")
+    assert a.exact_logit_rows >= 0.95 * a.rows
+    assert a.agreement >= 0.95
+    # weights of rows with the same expert set agree within one bf16 ulp
+    for t in range(a.rows):
+        if set(ti[t]) == set(f["index"][t]):
+            ours = dict(zip(ti[t].tolist(), oracle.bf16_float(tw[t]).tolist()))
+            hf = dict(zip(f["index"][t].tolist(), oracle.bf16_float(f["weights"][t]).tolist()))
+            for e, v in ours.items():
+                assert abs(v - hf[e]) <= abs(hf[e]) * 2.0 ** -7
