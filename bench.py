@@ -34,6 +34,10 @@ import time
 
 METRIC = ("verified tree tokens/s per MoE layer (1 GPU); achieved HBM GB/s + H2D GB/s")
 HBM_PEAK_GBS = 8000.0
+# Device sleep queued before each timed K3 launch of the recorded pass (about
+# 25 us of shader clock), so a launch enqueued on an idle compute stream is
+# timed from the device's start of the launch, not from the host's call.
+PARK_CYCLES = 50_000
 
 
 def log(msg: str) -> None:
@@ -293,7 +297,7 @@ def main_verify(args) -> int:
         rec = ops.LaunchRecorder(copies=False)
         rec_wall, rec_misses = 0.0, 0
         if recorded:
-            with ops.record_launches(copies=True) as rec:
+            with ops.record_launches(copies=True, park_cycles=PARK_CYCLES) as rec:
                 rec_wall, rec_misses, _, _ = run_steps(args.warmup + args.steps, rec)
     expert_bytes = experts.expert_bytes
     H = config.hidden_size
@@ -428,7 +432,7 @@ def main_sweep(args) -> int:
         rec = ops.LaunchRecorder(copies=False)
         rec_wall, rec_misses = 0.0, 0
         if recorded:
-            with ops.record_launches(copies=args.record == "full") as rec:
+            with ops.record_launches(copies=args.record == "full", park_cycles=PARK_CYCLES) as rec:
                 rec_wall, rec_misses, _, _ = run_steps(hidden[base + args.steps:], rec)
         ms = []
         for idx in idxs:
@@ -572,7 +576,7 @@ def main() -> int:
     rec = ops.LaunchRecorder(copies=False)
     rec_wall, rec_misses = 0.0, 0
     if args.record != "none":
-        with ops.record_launches(copies=args.record == "full") as rec:
+        with ops.record_launches(copies=args.record == "full", park_cycles=PARK_CYCLES) as rec:
             rec_wall, rec_misses, _ = run_steps(hidden[base + args.steps:], rec)
         log(f"recorded {args.steps} steps in {rec_wall * 1e3:.2f} ms: {rec_misses} misses")
 

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 7
+#define SF_ABI_VERSION 8
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -144,6 +144,13 @@ int sf_dispatch(const int64_t *topk_index, int tokens, int top_k,
  *   expert_ids      host int32 [n_experts]: experts computed by this call
  *   expert_weights  host uint64 [n_experts]: device address of each expert's
  *                   packed weights (a cache slot)
+ *   expert_row_begin, expert_row_count
+ *                   host int32 [n_experts] each, or both NULL: each listed
+ *                   expert's first permuted row and row count
+ *                   (offsets[e] and offsets[e+1] - offsets[e]).  A caller
+ *                   that has read the dispatch counts passes them, so the
+ *                   kernels start streaming weights without first reading
+ *                   offsets from device memory; with NULL they read them.
  *   act_workspace   bf16 [tokens * top_k, intermediate_size] scratch
  *   out_rows        bf16 [tokens * top_k, hidden_size] (rows of listed
  *                   experts are written, others untouched)
@@ -155,7 +162,9 @@ int sf_grouped_swiglu(const void *hidden, const int32_t *perm_pos,
                       int tokens, int top_k, int hidden_size,
                       int intermediate_size, int n_experts, int max_rows,
                       const int32_t *expert_ids,
-                      const uint64_t *expert_weights, void *act_workspace,
+                      const uint64_t *expert_weights,
+                      const int32_t *expert_row_begin,
+                      const int32_t *expert_row_count, void *act_workspace,
                       void *out_rows, sf_stream_t stream);
 
 /*

@@ -10,7 +10,7 @@ import threading
 
 from .build import LIB_PATH
 
-SF_ABI_VERSION = 7
+SF_ABI_VERSION = 8
 SF_ERR_HIP_BASE = 1000
 
 _lock = threading.Lock()
@@ -27,7 +27,8 @@ SIGNATURES = {
     "sf_error_string": ([_i], ctypes.c_char_p),
     "sf_router_topk": ([_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p], _i),
     "sf_dispatch": ([_p, _i, _i, _i, _p, _p, _p, _p, _p, _p], _i),
-    "sf_grouped_swiglu": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p], _i),
+    "sf_grouped_swiglu": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p],
+                          _i),
     "sf_grouped_swiglu_table": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _p, _p, _p], _i),
     "sf_grouped_swiglu_table_noalloc": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _p,
                                          _p], _i),

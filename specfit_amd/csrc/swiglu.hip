@@ -75,6 +75,12 @@ struct SwigluArgs {
   int64_t slot_stride;
   int32_t expert[kMaxListExperts];
   uint64_t wptr[kMaxListExperts];
+  // List mode with rows_known: first permuted row and row count of each
+  // listed expert, so a workgroup starts its weight stream without first
+  // reading offsets from memory.
+  int rows_known;
+  int32_t row0[kMaxListExperts];
+  int32_t rows[kMaxListExperts];
 };
 
 struct ExpertWork {
@@ -93,8 +99,13 @@ __device__ __forceinline__ bool resolve(const SwigluArgs& a, int j, ExpertWork& 
   }
   int e;
   if (R == Resolve::kList) {
-    e = a.expert[j];
     wk.w = reinterpret_cast<const uint16_t*>(a.wptr[j]);
+    if (a.rows_known) {
+      wk.r0 = a.row0[j];
+      wk.m = a.rows[j];
+      return wk.m > 0;
+    }
+    e = a.expert[j];
   } else {
     e = j;
     const int slot = a.slot_of_expert[e];
@@ -142,6 +153,7 @@ constexpr int kSteps = kBlockK / 32;  // MFMA k-steps per block
 // us: their A fragments of a third block cost registers).
 constexpr int kDepth = 2;
 constexpr int kDownDepth = 3;
+constexpr int kGateUpDepth = 2;  // 4 measured no faster (class 1 at 84 experts 6% slower)
 
 // Keeps the compiler's scheduler from moving instructions across this point,
 // so loads stay in issue order and registers hold only blocks in flight.
@@ -268,12 +280,22 @@ __device__ __forceinline__ void mfma_block_staged(const char* tile, char* stage,
 // acc = X . W^T over k-slice `slice` of KS (SP = kSteps/KS k-steps of each of
 // the NB blocks).  active: wave-uniform, false when the wavefront's tiles
 // have no rows (its A loads then hit one cache line, see a_rows).
-template <int NT, int MTW, int KS, int NB, int NP, int DP = kDepth>
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
+// after_issue runs once the prologue's loads are in flight (the place for
+// loads whose results are only needed after the stream, e.g. the epilogue's).
+// Weight blocks are loaded DW blocks ahead and token-row blocks DX <= DW
+// ahead (the token rows are L2 hits; the weights come from HBM).
+template <int NT, int MTW, int KS, int NB, int NP, int DW = kDepth, int DX = kDepth,
+          typename Hook = NoHook>
 __device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* const (&xr)[NP],
                                             int slice, bool active, char* smem, char* stage,
-                                            sf_f32x4 (&acc)[MTW][NT]) {
+                                            sf_f32x4 (&acc)[MTW][NT],
+                                            const Hook& after_issue = Hook{}) {
   constexpr bool kStaged = KS == 1 && MTW == 1 && NP == 4;
-  static_assert(NB >= DP, "fewer blocks than the prefetch depth");
+  static_assert(NB >= DW && DW >= DX, "prefetch depths exceed the block count");
   constexpr int SP = kSteps / KS;
   constexpr int kTile = 16 * NT * kRowBytes;
   const int lane = threadIdx.x & (SF_WAVE - 1);
@@ -283,32 +305,38 @@ __device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* c
   for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-  uint4 wr[DP][2 * NT];
-  uint4 xq[DP][MTW][SP];
+  uint4 wr[DW][2 * NT];
+  uint4 xq[DX][MTW][SP];
 #pragma unroll
-  for (int d = 0; d < DP; ++d) {
+  for (int d = 0; d < DW; ++d) {
     load_w<NT>(w, d, lane, wave, wr[d]);
-    if constexpr (kStaged) load_x_rows(xr, d, xq[d]);
-    else load_x<MTW, SP>(xr, d, s0, xq[d]);
+    if (d < DX) {
+      if constexpr (kStaged) load_x_rows(xr, d, xq[d % DX]);
+      else load_x<MTW, SP>(xr, d, s0, xq[d % DX]);
+    }
   }
+  SF_SCHED_FENCE();
+  after_issue();
+  SF_SCHED_FENCE();
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    const int d = b % DP;
+    const int dw = b % DW;
+    const int dx = b % DX;
     char* tile = smem + (b & 1) * kTile;
-    store_w<NT>(tile, lane, wave, wr[d]);
+    store_w<NT>(tile, lane, wave, wr[dw]);
     SF_SCHED_FENCE();
-    if (b + DP < NB) load_w<NT>(w, b + DP, lane, wave, wr[d]);
+    if (b + DW < NB) load_w<NT>(w, b + DW, lane, wave, wr[dw]);
     SF_SCHED_FENCE();
     __syncthreads();  // tile b visible; tile b-1's reads are done
     if constexpr (kStaged) {
-      if (active) mfma_block_staged<NT>(tile, stage, xq[d], lane, acc);
+      if (active) mfma_block_staged<NT>(tile, stage, xq[dx], lane, acc);
     } else {
-      if (active) mfma_block<NT, MTW, SP>(tile, s0, xq[d], lane, acc);
+      if (active) mfma_block<NT, MTW, SP>(tile, s0, xq[dx], lane, acc);
     }
     SF_SCHED_FENCE();
-    if (b + DP < NB) {
-      if constexpr (kStaged) load_x_rows(xr, b + DP, xq[d]);
-      else load_x<MTW, SP>(xr, b + DP, s0, xq[d]);
+    if (b + DX < NB) {
+      if constexpr (kStaged) load_x_rows(xr, b + DX, xq[dx]);
+      else load_x<MTW, SP>(xr, b + DX, s0, xq[dx]);
     }
     SF_SCHED_FENCE();
   }
@@ -416,12 +444,13 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
     if constexpr (KS == 1 && MTW == 1) {
       const uint16_t* xr[4];
       const bool active = a_rows_staged(row_of, mp, xr);
-      stream_gemm<NT, MTW, KS, NB, 4>(w, xr, 0, active, smem,
-                                       smem + 2 * 16 * NT * kRowBytes + wave * kStageBytes, acc);
+      stream_gemm<NT, MTW, KS, NB, 4, kGateUpDepth>(
+          w, xr, 0, active, smem, smem + 2 * 16 * NT * kRowBytes + wave * kStageBytes, acc);
     } else {
       const uint16_t* xr[MTW];
       const bool active = a_rows<MTW, TM>(row_of, mp, xr);
-      stream_gemm<NT, MTW, KS, NB, MTW>(w, xr, wave / TM, active, smem, nullptr, acc);
+      stream_gemm<NT, MTW, KS, NB, MTW, kGateUpDepth>(w, xr, wave / TM, active, smem, nullptr,
+                                                      acc);
     }
     bool owner = true;
     if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
@@ -495,8 +524,35 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
     const uint16_t* ar[MTW];
     const bool active = a_rows<MTW, TM>(
         [&](int row) { return a.act + static_cast<int64_t>(wk.r0 + p0 + row) * I; }, mp, ar);
+    // Routing weights of this lane's output rows.  The epilogue used to
+    // read perm_pos and then route_w for each row after the stream (two
+    // dependent global latencies per row at the end of a short workgroup);
+    // here perm_pos is read before the stream's first loads and route_w
+    // right after them, so both latencies overlap the weight stream.
+    int pos[MTW][4];
+    float rw[MTW][4];
+    const bool scaled = a.route_w != nullptr;
+    if (scaled) {
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = min((mt * TM + wave % TM) * 16 + 4 * (lane >> 4) + i, mp - 1);
+          pos[mt][i] = a.perm_pos[wk.r0 + p0 + row];
+        }
+    }
+    SF_SCHED_FENCE();
     sf_f32x4 acc[MTW][NT];
-    stream_gemm<NT, MTW, KS, NB, MTW, (KS == 4 && NB >= kDownDepth ? kDownDepth : kDepth)>(w, ar, wave / TM, active, smem, nullptr, acc);
+    stream_gemm<NT, MTW, KS, NB, MTW, (NB < kDownDepth ? NB : kDownDepth),
+                (KS == 4 && NB >= kDownDepth ? kDownDepth : kDepth)>(
+        w, ar, wave / TM, active, smem, nullptr, acc, [&] {
+          if (scaled) {
+#pragma unroll
+            for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) rw[mt][i] = sf_bf16_to_f32(a.route_w[pos[mt][i]]);
+          }
+        });
     bool owner = true;
     if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
     if (!owner) continue;
@@ -507,11 +563,10 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
         const int row = (mt * TM + wave % TM) * 16 + 4 * (lane >> 4) + i;
         if (row < mp) {
           const int r = wk.r0 + p0 + row;
-          const float rw = a.route_w ? sf_bf16_to_f32(a.route_w[a.perm_pos[r]]) : 1.f;
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) {
             float y = sf_round_bf16(acc[mt][nt][i]);
-            if (a.route_w) y = y * rw;
+            if (scaled) y = y * rw[mt][i];
             a.out[static_cast<int64_t>(r) * a.H + n0 + 16 * nt + (lane & 15)] = sf_f32_to_bf16(y);
           }
         }
@@ -670,6 +725,8 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
                                  int intermediate_size, int n_experts, int max_rows,
                                  const int32_t* expert_ids,
                                  const uint64_t* expert_weights,
+                                 const int32_t* expert_row_begin,
+                                 const int32_t* expert_row_count,
                                  void* act_workspace, void* out_rows,
                                  sf_stream_t stream) {
   int rc = check_common(tokens, top_k, hidden_size, intermediate_size);
@@ -679,6 +736,14 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
   if (!hidden || !perm_pos || !offsets || !expert_ids || !expert_weights ||
       !act_workspace || !out_rows)
     return SF_ERR_INVALID_ARGUMENT;
+  if ((expert_row_begin == nullptr) != (expert_row_count == nullptr)) return SF_ERR_INVALID_ARGUMENT;
+  const bool rows_known = expert_row_begin != nullptr;
+  for (int i = 0; rows_known && i < n_experts; ++i) {
+    const long long end = static_cast<long long>(expert_row_begin[i]) + expert_row_count[i];
+    if (expert_row_begin[i] < 0 || expert_row_count[i] < 0 ||
+        end > static_cast<long long>(tokens) * top_k)
+      return SF_ERR_INVALID_ARGUMENT;
+  }
   bool aligned = aligned16(hidden) && aligned16(act_workspace);
   for (int i = 0; i < n_experts; ++i) {
     if (expert_ids[i] < 0 || expert_weights[i] == 0) return SF_ERR_INVALID_ARGUMENT;
@@ -699,9 +764,14 @@ extern "C" int sf_grouped_swiglu(const void* hidden, const int32_t* perm_pos,
     a.H = hidden_size;
     a.I = intermediate_size;
     a.n = n_experts - base < kMaxListExperts ? n_experts - base : kMaxListExperts;
+    a.rows_known = rows_known ? 1 : 0;
     for (int i = 0; i < a.n; ++i) {
       a.expert[i] = expert_ids[base + i];
       a.wptr[i] = expert_weights[base + i];
+      if (rows_known) {
+        a.row0[i] = expert_row_begin[base + i];
+        a.rows[i] = expert_row_count[base + i];
+      }
     }
     rc = launch<Resolve::kList>(a, a.n, shape, max_rows, s);
     if (rc) return rc;

@@ -110,8 +110,14 @@ class LaunchRecorder:
     the stream the work runs on (enabled by ``record_launches``).  Events
     are TimingEvents; read them after the device has finished the work."""
 
-    def __init__(self, *, copies: bool = True) -> None:
+    def __init__(self, *, copies: bool = True, park_cycles: int = 0) -> None:
         self.k3: list[tuple[int, int, str, TimingEvent, TimingEvent]] = []
+        # With park_cycles, a short device sleep is queued on the stream
+        # before each launch's start event: a launch enqueued while its
+        # stream is idle would otherwise have the host's enqueue latency
+        # (the time between the start event and the kernels reaching the
+        # device) counted as kernel time.
+        self.park_cycles = park_cycles
         # Copies are timed per window (first copy start .. last copy end of a
         # window, per stream), not per copy: ``close_copy_window`` ends one.
         self.copies = copies
@@ -158,10 +164,12 @@ class LaunchRecorder:
             total += cur_e - cur_s
         return total * 1e-3
 
-    @staticmethod
-    def _events(stream):
+    def _events(self, stream):
         start = TimingEvent()
         end = TimingEvent()
+        if self.park_cycles:
+            with torch.cuda.stream(stream):
+                torch.cuda._sleep(self.park_cycles)
         start.record(stream)
         return start, end
 
@@ -172,14 +180,15 @@ _recorder: LaunchRecorder | None = None
 class record_launches:
     """Context manager: ``with record_launches() as rec: ...``."""
 
-    def __init__(self, *, copies: bool = True) -> None:
+    def __init__(self, *, copies: bool = True, park_cycles: int = 0) -> None:
         self._copies = copies
+        self._park = park_cycles
 
     def __enter__(self) -> LaunchRecorder:
         global _recorder
         if _recorder is not None:
             raise RuntimeError("launch recording is already active")
-        _recorder = LaunchRecorder(copies=self._copies)
+        _recorder = LaunchRecorder(copies=self._copies, park_cycles=self._park)
         return _recorder
 
     def __exit__(self, *exc) -> None:
@@ -252,8 +261,10 @@ class DispatchPlan:
     perm_pos: torch.Tensor
     inv_perm: torch.Tensor
     host_counts: torch.Tensor | None = None
-    # Python copy of host_counts[0] (routes per expert), made with it.
+    # Python copies of host_counts[0] (routes per expert) and [1] (offsets),
+    # made with it.
     count_list: list | None = None
+    offset_list: list | None = None
     _counts_event: tuple | None = None  # (event, staging) of a started read
 
     @property
@@ -299,7 +310,7 @@ class DispatchPlan:
             ev.synchronize()
             self._counts_event = None
             self.host_counts = staging
-            self.count_list = staging[0].tolist()
+            self.count_list, self.offset_list = staging.tolist()
         return self.host_counts
 
     def active_experts(self) -> tuple[int, ...]:
@@ -340,7 +351,7 @@ def dispatch(index: torch.Tensor, num_experts: int, *,
         if host_meta is not None:
             host_meta.zero_()
             plan.host_counts = host_meta
-            plan.count_list = host_meta[0].tolist()
+            plan.count_list, plan.offset_list = host_meta.tolist()
         return plan
     handle = _stream_handle(stream, dev)
     counts_ptr = meta.data_ptr()  # row 0; row 1 (offsets) follows E + 1 int32 later
@@ -413,18 +424,25 @@ def grouped_swiglu(hidden: torch.Tensor, plan: DispatchPlan, route_weights: torc
         ptrs = [w.data_ptr() for w in weights]
     id_arr = (ctypes.c_int32 * n)(*ids)
     w_arr = (ctypes.c_uint64 * n)(*ptrs)
-    rec = _recorder
-    if rec is not None:
-        s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
-        start, end = rec._events(s)
+    # Rows of each expert from the counts already on the host: the kernels
+    # then start streaming weights without reading offsets first.
+    row_begin = row_count = None
+    offs = plan.offset_list
+    if counts is not None and offs is not None:
+        row_begin = ctypes.cast((ctypes.c_int32 * n)(*[offs[e] for e in ids]), ctypes.c_void_p)
+        row_count = ctypes.cast((ctypes.c_int32 * n)(*[counts[e] for e in ids]), ctypes.c_void_p)
     max_rows = N
     if counts is not None:
         max_rows = max(1, max(counts[e] for e in ids))
+    rec = _recorder
+    if rec is not None:  # timing events bracket the C call only, not the host work above
+        s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
+        start, end = rec._events(s)
     rc = _native.lib().sf_grouped_swiglu(
         _ptr(hidden), _ptr(plan.perm_pos), _ptr(plan.offsets), _ptr(route_weights),
         plan.tokens, plan.top_k, hidden_size, intermediate_size, n, max_rows,
         ctypes.cast(id_arr, ctypes.c_void_p), ctypes.cast(w_arr, ctypes.c_void_p),
-        _ptr(act), _ptr(out_rows), _stream_handle(stream, hidden.device))
+        row_begin, row_count, _ptr(act), _ptr(out_rows), _stream_handle(stream, hidden.device))
     _native.check(rc, "sf_grouped_swiglu")
     if rec is not None:
         end.record(s)

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_error_strings():
-    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 7
+    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 8
     assert _native.error_string(0) == "success"
     assert _native.error_string(1) == "invalid argument"
     assert _native.error_string(12345) != ""
@@ -57,7 +57,7 @@ def test_host_side_validation_needs_no_device():
     assert lib.sf_dispatch(null, 4, 8, 300, null, null, null, null, null, null) == 1
     assert lib.sf_combine(null, null, null, null, 4, 64, 128, 2048, 0, null, null) == 1
     assert lib.sf_grouped_swiglu(null, null, null, null, 4, 8, 2048, 768, -1, 1, null, null, null,
-                                 null, null) == 1
+                                 null, null, null, null) == 1
     assert lib.sf_expert_swiglu(null, 4, 10, 2048, 768, null, null, null, null) == 1
     # tree attention: bad counts, heads not a multiple, head dim, misaligned keys
     fake = 4096  # never dereferenced: every case below fails before a launch
