@@ -235,9 +235,13 @@ def router_topk(hidden: torch.Tensor, weight: torch.Tensor, top_k: int,
     weight = weight.contiguous()
     T, H = hidden.shape
     E = weight.shape[0]
-    logits = torch.empty((T, E), dtype=_BF16, device=hidden.device)
-    w = torch.empty((T, top_k), dtype=_BF16, device=hidden.device)
-    idx = torch.empty((T, top_k), dtype=torch.int64, device=hidden.device)
+    # One allocation for the three outputs (indices first, 8-byte aligned).
+    nk = T * top_k
+    buf = torch.empty(nk + (T * E + nk + 3) // 4, dtype=torch.int64, device=hidden.device)
+    idx = buf[:nk].view(T, top_k)
+    halves = buf[nk:].view(_BF16)
+    logits = halves[:T * E].view(T, E)
+    w = halves[T * E:T * E + nk].view(T, top_k)
     rc = _native.lib().sf_router_topk(
         _ptr(hidden), _ptr(weight), T, H, E, int(top_k), int(bool(norm_topk_prob)),
         _ptr(logits), _ptr(w), _ptr(idx), _stream_handle(stream, hidden.device))
@@ -342,9 +346,12 @@ def dispatch(index: torch.Tensor, num_experts: int, *,
     index = index.contiguous()
     T, K = index.shape
     dev = index.device
-    meta = torch.empty(shape, dtype=torch.int32, device=dev)
-    perm = torch.empty(T * K, dtype=torch.int32, device=dev)
-    inv = torch.empty(T * K, dtype=torch.int32, device=dev)
+    # [counts; offsets], perm_pos and inv_perm in one allocation.
+    e1 = num_experts + 1
+    buf = torch.empty(2 * e1 + 2 * T * K, dtype=torch.int32, device=dev)
+    meta = buf[:2 * e1].view(2, e1)
+    perm = buf[2 * e1:2 * e1 + T * K]
+    inv = buf[2 * e1 + T * K:]
     plan = DispatchPlan(T, K, int(num_experts), meta, perm, inv)
     if T * K == 0:
         meta.zero_()

@@ -137,6 +137,7 @@ class _Slot:
     # raw handle of a stream that read the slot -> event after its last read
     use_events: dict = field(default_factory=dict)
     write_stream: torch.cuda.Stream | None = None  # stream of the last H2D into the slot
+    ready_seq: int = -1  # submission sequence of that H2D (the one ready_event marks)
 
     def victim_rank(self) -> tuple:
         return (self.expert_id is not None, self.last_used_sequence, self.slot_id)
@@ -452,8 +453,11 @@ class GpuExpertCache:
             self._touch(slot)
         else:
             self._state_version += 1
-        return ExpertLease(self, slot.expert_id, slot.slot_id, slot.generation, slot.ready_event,
-                           touch_pending=not touch_now, ready_known=ready_known)
+        lease = ExpertLease(self, slot.expert_id, slot.slot_id, slot.generation, slot.ready_event,
+                            touch_pending=not touch_now, ready_known=ready_known)
+        lease._ready_stream = slot.write_stream
+        lease._ready_seq = slot.ready_seq
+        return lease
 
     @staticmethod
     def _check_pin(slot: _Slot, key: Hashable, generation: int) -> None:
@@ -671,6 +675,7 @@ class GpuExpertCache:
             s.expert_id = None
             s.ready_event = None
             s.write_stream = None
+            s.ready_seq = -1
             s.use_events.clear()
 
     def cold_reset(self) -> None:
@@ -714,7 +719,7 @@ class GpuExpertCache:
         for s, (expert, gen, last, ready, guards, leases) in zip(self._slots, image.slots):
             s.expert_id, s.generation, s.last_used_sequence = expert, gen, last
             s.ready_event, s.use_events, s.active_leases = ready, dict(guards), leases
-            s.write_stream = None
+            s.write_stream, s.ready_seq = None, -1
         self._resident = _ResidentMap(image.resident)
         self._inflight = dict(image.inflight)
         self._outstanding_transfers = deque(image.transfers)
@@ -841,6 +846,7 @@ class GpuExpertCache:
         ready.record(stream)
         slot.ready_event = ready
         slot.write_stream = stream
+        slot.ready_seq = self._submission_sequence
         transfer = _Transfer(key, slot.slot_id, slot.generation, self._submission_sequence, ready)
         self._inflight[key] = transfer
         self._outstanding_transfers.append(transfer)

@@ -51,7 +51,7 @@ class ExpertLease:
     """One leased slot generation (see the module docstring)."""
 
     __slots__ = ("_cache", "_key", "_generation", "_state", "_readers", "_touch_pending",
-                 "_ready_known", "ready_event", "slot_id")
+                 "_ready_known", "_ready_stream", "_ready_seq", "ready_event", "slot_id")
 
     def __init__(self, cache: "GpuExpertCache", key: Hashable, slot_id: int, generation: int,
                  ready_event: torch.cuda.Event, *, touch_pending: bool = False,
@@ -67,6 +67,10 @@ class ExpertLease:
         # True when the ready event is known complete (a resident hit): the
         # wait then queues no stream dependency.
         self._ready_known = ready_known
+        # Stream and cache submission sequence of the transfer that records
+        # ready_event (set by the cache; None when unknown).
+        self._ready_stream = None
+        self._ready_seq = -1
         self.slot_id = slot_id
         self.ready_event = ready_event
 
@@ -94,6 +98,25 @@ class ExpertLease:
             stream.wait_event(self.ready_event)
         self._readers[int(stream.cuda_stream)] = stream
         return cache._consume(self, stream)
+
+    def _wait_pending(self, stream: torch.cuda.Stream, pending: dict) -> torch.Tensor:
+        """``wait`` for a batched launch: instead of queueing the stream wait
+        now, keep in ``pending`` (transfer stream -> (sequence, event)) the
+        latest transfer event per copy stream; the launch that reads the
+        batch waits on those only (transfers on one stream complete in
+        order).  Everything else -- readers, touch, observer -- as ``wait``."""
+        if self._state != _OPEN:
+            raise RuntimeError("cannot wait on a released expert lease")
+        if not self._ready_known:
+            key = self._ready_stream
+            if key is None:
+                stream.wait_event(self.ready_event)
+            else:
+                held = pending.get(key)
+                if held is None or held[0] < self._ready_seq:
+                    pending[key] = (self._ready_seq, self.ready_event)
+        self._readers[int(stream.cuda_stream)] = stream
+        return self._cache._consume(self, stream)
 
     def release(self) -> None:
         """Record use guards on the consuming streams and drop the pin.

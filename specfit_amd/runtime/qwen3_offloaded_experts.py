@@ -36,7 +36,7 @@ invariant to order, slot count and prefetch policy.
 from __future__ import annotations
 
 from contextlib import closing
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from enum import Enum
 from itertools import compress
 from typing import Sequence
@@ -79,6 +79,9 @@ class _GroupedRoutes:
     tag: str = ""                 # "resident" or "miss": label of the launch
     storage: torch.Tensor | None = None  # the cache's [slots, 3*I*H] slot storage
     covered: frozenset = frozenset()  # experts whose rows a slot-table launch computed
+    # Transfers the next launch must wait for: copy stream -> (sequence,
+    # ready event) of the latest transfer of a batched lease on that stream.
+    pending: dict = field(default_factory=dict)
 
 
 def _dispatch(top_k_index: torch.Tensor, num_experts: int,
@@ -348,12 +351,14 @@ class Qwen3OffloadedExperts(nn.Module):
     def _new_routes(self, hidden_states, top_k_weights, plan) -> _GroupedRoutes:
         T, K = top_k_weights.shape
         dev = hidden_states.device
+        N, I, H = T * K, self.intermediate_size, self.hidden_size
+        work = torch.empty(N * (I + H), dtype=torch.bfloat16, device=dev)  # act, then rows
         routes = _GroupedRoutes(
             hidden=hidden_states.contiguous(),
             plan=plan,
             route_weights=top_k_weights.to(torch.bfloat16).contiguous().reshape(-1),
-            act=torch.empty((T * K, self.intermediate_size), dtype=torch.bfloat16, device=dev),
-            rows=torch.empty((T * K, self.hidden_size), dtype=torch.bfloat16, device=dev))
+            act=work[:N * I].view(N, I),
+            rows=work[N * I:].view(N, H))
         storage = self.cache.storage
         if storage.dim() == 2 and storage.shape[1] == 3 * self.hidden_size * self.intermediate_size:
             routes.storage = storage
@@ -381,6 +386,12 @@ class Qwen3OffloadedExperts(nn.Module):
             covered = routes.covered
             todo = [(e, w) for e, _, w in batch if e not in covered] if covered else \
                 [(e, w) for e, _, w in batch]
+            pending = routes.pending
+            if pending:
+                stream = torch.cuda.current_stream(self.cache.device)
+                for _, ready in pending.values():
+                    stream.wait_event(ready)
+                pending.clear()
             if todo:
                 routes.expert_ids = [e for e, _ in todo]
                 routes.tag = tag
@@ -460,7 +471,7 @@ class Qwen3OffloadedExperts(nn.Module):
                             ahead_missed = will_miss
                         except NoEvictableSlotError:
                             pass
-                    weights = current.wait(stream)
+                    weights = current._wait_pending(stream, routes.pending)
                 except BaseException:
                     current.release()
                     raise

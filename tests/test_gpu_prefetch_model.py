@@ -519,3 +519,33 @@ def test_packed_checkpoint_loads_bitwise_equal_to_original(device):
         with pytest.raises(PackedCheckpointError, match="config SHA256"):
             load_offloaded_qwen3(original, device=device, slots_per_layer=2,
                                  packed_checkpoint_root=packed_root)
+
+
+def test_one_at_a_time_experts_protocol_matches_batches(device):
+    """The reference's scheduler protocol (``experts``: one (id, lease) per
+    step, released on resume) gives the same outputs and statistics as the
+    batched protocol the layer uses, with and without predictions."""
+    from specfit_amd.runtime import Qwen3ExpertPrefetch
+
+    loaded, _, inputs = _case(slots=3)
+    expected = loaded.model(*inputs)
+    single = lambda self, layer, active: ([pair] for pair in self.experts(layer, active))
+    for prediction in ((), (0, 1, 2, 3, 4)):
+        results = []
+        for one_at_a_time in (False, True):
+            loaded.cold_reset_expert_caches()
+            ctx = loaded.prefetch_experts({i: prediction for i in range(2)}, lookahead_layers=1,
+                                          trace=True)
+            patcher = patch.object(Qwen3ExpertPrefetch, "expert_batches", single) \
+                if one_at_a_time else ExitStack()
+            with patcher, ctx as sched:
+                actual = loaded.model(*inputs)
+            torch.cuda.synchronize()
+            assert torch.equal(actual, expected), (prediction, one_at_a_time)
+            st = sched.stats()
+            assert st["complete"]
+            results.append([(r["actual_experts"], r["computed_experts"]) for r in st["layers"]])
+            computes = [e for e in sched.events() if e["action"] == "compute"]
+            assert len(computes) == 10  # five experts in each of two layers
+        assert results[0] == results[1]
+    _close(loaded)
