@@ -73,9 +73,12 @@ def parse_args():
                    help="48-layer forwards only. layer: each MoE layer's own resident-first, "
                         "one-ahead sequence; ready_demand: the predicted-prefetch scheduler "
                         "(Qwen3ExpertPrefetch) with no predictions, the reference's measured "
-                        "decode executor; predicted (cold48 only): the scheduler given each "
-                        "forward's own routed experts as predictions (captured in an untimed run "
-                        "of the same forward: an upper bound for a draft's predictions)")
+                        "decode executor; predicted: the scheduler given each forward's own "
+                        "routed experts as predictions (captured in untimed runs of the same "
+                        "forwards before the warm-up: an upper bound for a draft's predictions)")
+    p.add_argument("--lookahead", type=int, default=None,
+                   help="the scheduler's lookahead_layers (default 0 for ready_demand, as the "
+                        "reference's measured decode calls it; 1 for predicted)")
     p.add_argument("--max-inflight", type=int, default=2,
                    help="the scheduler's bound on incomplete transfers (default 2, the "
                         "reference's default)")
@@ -85,8 +88,8 @@ def parse_args():
     args = p.parse_args()
     if args.executor != "layer" and args.workload not in ("verify48", "cold48"):
         p.error("--executor applies to the 48-layer forwards (verify48, cold48)")
-    if args.executor == "predicted" and args.workload != "cold48":
-        p.error("--executor predicted needs cold48 (its capture run would warm verify48's caches)")
+    if args.lookahead is None:
+        args.lookahead = 1 if args.executor == "predicted" else 0
     if args.steps is None:
         args.steps = 10 if args.workload in ("verify48", "cold48") else 50
     return args
@@ -242,6 +245,9 @@ def main_verify(args) -> int:
         finally:
             for h in hooks:
                 h.remove()
+        # Routes do not depend on cache contents; start the measured
+        # forwards from the empty caches every other executor starts from.
+        loaded.cold_reset_expert_caches()
         log(f"captured the routed experts of {n} forwards")
     sched_stats = []
 
@@ -249,7 +255,7 @@ def main_verify(args) -> int:
         if executor == "layer":
             res = verify_draft_tree(target, trees[i], seeds[i], cache, commit=False)
         else:
-            with loaded.prefetch_experts(predictions[i], lookahead_layers=1,
+            with loaded.prefetch_experts(predictions[i], lookahead_layers=args.lookahead,
                                          max_inflight=args.max_inflight) as sched:
                 res = verify_draft_tree(target, trees[i], seeds[i], cache, commit=False)
             sched_stats.append(sched.stats())
@@ -352,7 +358,7 @@ def main_verify(args) -> int:
         timed = sched_stats[args.warmup:args.warmup + args.steps]
         rows = [row for st in timed for row in st["layers"]]
         line["scheduler"] = {
-            "lookahead_layers": 1, "max_inflight": args.max_inflight,
+            "lookahead_layers": args.lookahead, "max_inflight": args.max_inflight,
             "complete": all(st["complete"] for st in timed),
             "peak_inflight": max(st["peak_inflight"] for st in timed),
             "queue_capacity_waits": sum(st["queue_capacity_waits"] for st in timed) / len(timed),
