@@ -162,14 +162,17 @@ def test_bench_refuses_more_than_one_gpu():
     assert out.returncode == 2 and "one GPU only" in out.stderr and not out.stdout.strip()
 
 
-@pytest.mark.parametrize("argv,ok", [(["--executor", "ready_demand"], False),
-                                     (["--workload", "verify48", "--executor", "predicted"], False),
-                                     (["--workload", "verify48", "--executor", "ready_demand"], True),
-                                     (["--workload", "cold48", "--executor", "predicted"], True)])
-def test_bench_executor_applies_to_the_48_layer_forwards(monkeypatch, argv, ok):
+@pytest.mark.parametrize("argv,ok,lookahead", [
+    (["--executor", "ready_demand"], False, None),
+    (["--workload", "verify48", "--executor", "predicted"], True, 1),
+    (["--workload", "verify48", "--executor", "ready_demand"], True, 0),
+    (["--workload", "cold48", "--executor", "predicted"], True, 1),
+    (["--workload", "cold48", "--executor", "ready_demand", "--lookahead", "2"], True, 2)])
+def test_bench_executor_applies_to_the_48_layer_forwards(monkeypatch, argv, ok, lookahead):
     monkeypatch.setattr(sys, "argv", ["bench.py", *argv])
     if ok:
-        assert bench.parse_args().executor == argv[-1]
+        args = bench.parse_args()
+        assert args.executor == argv[3] and args.lookahead == lookahead
     else:
         with pytest.raises(SystemExit):
             bench.parse_args()
