@@ -32,6 +32,7 @@ def _hip():
                                             ctypes.c_void_p]
         lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
         lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        lib.hipEventQuery.argtypes = [ctypes.c_void_p]
         _hip_runtime = lib
     return _hip_runtime
 
@@ -69,6 +70,7 @@ class TimingEvent:
 
 
 _HIP_EVENT_DISABLE_TIMING = 0x2  # hip_runtime_api.h
+_HIP_ERROR_NOT_READY = 600       # hipErrorNotReady
 
 
 class HostWaitEvent:
@@ -98,6 +100,15 @@ class HostWaitEvent:
         rc = _hip().hipEventSynchronize(self._ev)
         if rc:
             raise RuntimeError(f"hipEventSynchronize failed ({rc})")
+
+    def query(self) -> bool:
+        """True once the recorded work has completed (does not block)."""
+        rc = _hip().hipEventQuery(self._ev)
+        if rc == _HIP_ERROR_NOT_READY:
+            return False
+        if rc:
+            raise RuntimeError(f"hipEventQuery failed ({rc})")
+        return True
 
     def __del__(self) -> None:
         if self._ev is not None:
@@ -279,16 +290,16 @@ class DispatchPlan:
     def offsets(self) -> torch.Tensor:
         return self.meta[1]
 
-    def fetch_counts(self, staging: torch.Tensor | None = None) -> torch.Tensor:
+    def fetch_counts(self, staging: torch.Tensor | None = None, *, idle=None) -> torch.Tensor:
         """[counts; offsets] in pinned host memory: waits for dispatch when it
         wrote them there (``dispatch(..., host_meta=...)``), else copies them
         in one transfer and waits for it.  ``staging`` is a reusable pinned
         int32 [2, E+1] buffer for the copy; without one a pinned buffer is
         allocated (which may synchronise the device while the allocator
-        grows, so hot paths pass one)."""
+        grows, so hot paths pass one).  ``idle``: see ``finish_counts``."""
         if self.host_counts is None:
             self.start_counts(staging)
-        return self.finish_counts()
+        return self.finish_counts(idle)
 
     def start_counts(self, staging: torch.Tensor | None = None) -> None:
         """Enqueue the [counts; offsets] copy on the current stream without
@@ -306,11 +317,18 @@ class DispatchPlan:
         ev.record(torch.cuda.current_stream(self.meta.device))
         self._counts_event = (ev, staging)
 
-    def finish_counts(self) -> torch.Tensor:
+    def finish_counts(self, idle=None) -> torch.Tensor:
+        """Wait for the counts.  ``idle``, when given, is called repeatedly
+        while they are not there yet, as long as it returns True (host work
+        that should not wait for the routes, e.g. submitting copies as copy
+        credits free up); then the host blocks."""
         if self.host_counts is None:
             if self._counts_event is None:
                 self.start_counts()
             ev, staging = self._counts_event
+            if idle is not None:
+                while not ev.query() and idle():
+                    pass
             ev.synchronize()
             self._counts_event = None
             self.host_counts = staging

@@ -42,6 +42,11 @@ How this build runs it (MI355X host path):
   launch and releases together (one use-guard event for the batch).
   ``experts`` keeps the reference's one-expert-at-a-time protocol.
 * Each layer's queue, holdings and counters live in a ``_LayerPlan``.
+* While a layer's router counts are on their way to the host, the layer
+  keeps calling ``_place_while_routing``, which places requests as queue
+  credits free up (the attention hook's placement, repeated).  Otherwise
+  the copy link idles from the previous layer's last copy until the routes
+  arrive; the decisions are the same, only earlier.
 
 Batches change when leases are released relative to the scheduler's own
 decisions (a batch's leases are released together, after its launch), not
@@ -411,6 +416,21 @@ class Qwen3ExpertPrefetch:
         for plan in self._plans[self._current:stop]:
             if not self._place(plan):
                 return
+
+    def _place_while_routing(self) -> bool:
+        """Called by the open layer while its router's counts are on their
+        way to the host: place what the queue credits allow, as the
+        attention hook does.  True while a placement waits for a credit
+        (the caller polls again), False when nothing more can be placed
+        before the routes arrive (the caller then blocks)."""
+        if self._open_layer is None:
+            return False
+        self._pump()
+        if self._in_flight() < self.max_inflight:
+            return False
+        stop = min(len(self._plans), self._current + self.lookahead_layers + 1)
+        return any(plan.requests and (plan.routed is not None or plan.held < plan.limit)
+                   for plan in self._plans[self._current:stop])
 
     def _place(self, plan: _LayerPlan) -> bool:
         demand = plan.routed is not None

@@ -281,8 +281,12 @@ class Qwen3OffloadedExperts(nn.Module):
         transfers first) in batches; each batch is computed by one grouped K3
         launch, enqueued before control returns to the scheduler, which then
         releases the batch's leases.  Outputs are reduced canonically."""
-        routes, active = self._prepare(hidden_states, top_k_index, top_k_weights)
         scheduler = self._prediction_scheduler
+        # While the device routes, the scheduler keeps placing copies as
+        # queue credits free up (the copy link would otherwise idle until
+        # the counts arrive).
+        routes, active = self._prepare(hidden_states, top_k_index, top_k_weights,
+                                       idle=scheduler._place_while_routing)
         batches = scheduler.expert_batches(self.layer_id, active)
         stream = torch.cuda.current_stream(self.cache.device)
         with closing(batches):
@@ -316,10 +320,11 @@ class Qwen3OffloadedExperts(nn.Module):
             self._num_experts = n
         return self._num_experts
 
-    def _prepare(self, hidden_states, top_k_index, top_k_weights):
+    def _prepare(self, hidden_states, top_k_index, top_k_weights, idle=None):
         """Dispatch on the device, read the active experts, allocate the
         layer's row buffers.  Returns (routes or None when there are no
-        routes, active experts ascending)."""
+        routes, active experts ascending).  ``idle``: host work to run while
+        the counts are not there yet (``DispatchPlan.finish_counts``)."""
         T, K = top_k_index.shape
         if hidden_states.dtype != torch.bfloat16:
             raise ValueError("hidden_states must be bfloat16")
@@ -330,7 +335,7 @@ class Qwen3OffloadedExperts(nn.Module):
         # The row buffers do not depend on the counts: allocate them while
         # the device routes.
         routes = self._new_routes(hidden_states, top_k_weights, plan)
-        counts = self._read_counts(plan, top_k_index, num_experts)
+        counts = self._read_counts(plan, top_k_index, num_experts, idle)
         active = tuple(compress(range(num_experts), counts))
         return routes, active
 
@@ -340,9 +345,9 @@ class Qwen3OffloadedExperts(nn.Module):
                                             pin_memory=True)
         return self._host_counts
 
-    def _read_counts(self, plan, top_k_index, num_experts) -> list:
+    def _read_counts(self, plan, top_k_index, num_experts, idle=None) -> list:
         """The layer's one device-to-host read: routes per expert."""
-        plan.fetch_counts(self._counts_staging(num_experts))
+        plan.fetch_counts(self._counts_staging(num_experts), idle=idle)
         counts = plan.count_list
         if counts[num_experts]:
             self._raise_invalid_index(top_k_index, num_experts)

@@ -549,3 +549,31 @@ def test_one_at_a_time_experts_protocol_matches_batches(device):
             assert len(computes) == 10  # five experts in each of two layers
         assert results[0] == results[1]
     _close(loaded)
+
+
+def test_predictions_keep_copying_while_the_router_result_is_awaited(device):
+    """With one queue credit, the attention hook can place only the first
+    prediction.  The layer's counts read then waits for a slow device (a
+    sleep queued before the layer's dispatch); meanwhile the scheduler places
+    the other predictions as the credit frees, so all of them are ready when
+    the routes arrive.  Outputs are unchanged."""
+    loaded, _, inputs = _case(slots=4, layers=1)
+    expected = loaded.model(*inputs)
+    module = loaded.model.model.layers[0].mlp.experts
+    hook = module.register_forward_pre_hook(lambda mod, args: torch.cuda._sleep(50_000_000))
+    try:
+        loaded.cold_reset_expert_caches()
+        with loaded.prefetch_experts({0: (0, 1, 2)}, lookahead_layers=0, max_inflight=1,
+                                     trace=True) as sched:
+            actual = loaded.model(*inputs)
+        torch.cuda.synchronize()
+    finally:
+        hook.remove()
+    assert torch.equal(actual, expected)
+    row = sched.stats()["layers"][0]
+    assert row["prediction_copies"] == 3 and row["ready_at_router"] == 3, row
+    assert row["demand_copies"] == 2  # experts 3 and 4
+    events = sched.events()
+    routed = next(i for i, e in enumerate(events) if e["action"] == "router")
+    assert [e["expert_id"] for e in events[:routed] if e["action"] == "copy"] == [0, 1, 2]
+    _close(loaded)
