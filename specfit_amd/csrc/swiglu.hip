@@ -124,6 +124,20 @@ __device__ __forceinline__ const uint16_t* row_ptr(const SwigluArgs& a, int r) {
   return a.hidden + static_cast<int64_t>(tok) * a.row_stride;
 }
 
+// row_ptr in two steps: token_fetch issues the load of permuted row r's
+// route position (dense mode: r itself), token_ptr turns the value into the
+// token's hidden row.
+template <Resolve R>
+__device__ __forceinline__ int token_fetch(const SwigluArgs& a, int r) {
+  return R == Resolve::kDense ? r : a.perm_pos[r];
+}
+
+template <Resolve R>
+__device__ __forceinline__ const uint16_t* token_ptr(const SwigluArgs& a, int v) {
+  const int tok = R == Resolve::kDense ? v : v / a.top_k;
+  return a.hidden + static_cast<int64_t>(tok) * a.row_stride;
+}
+
 __device__ __forceinline__ sf_bf16x8 as_bf16x8(uint4 v) {
   return __builtin_bit_cast(sf_bf16x8, v);
 }
@@ -279,18 +293,25 @@ __device__ __forceinline__ void mfma_block_staged(const char* tile, char* stage,
 
 // acc = X . W^T over k-slice `slice` of KS (SP = kSteps/KS k-steps of each of
 // the NB blocks).  active: wave-uniform, false when the wavefront's tiles
-// have no rows (its A loads then hit one cache line, see a_rows).
+// have no rows (its A loads then hit one cache line, see a_fetch).
 struct NoHook {
   __device__ void operator()() const {}
 };
 
+// make_xr(xr) fills the NP token-row pointers of the lane.  With kLateX it
+// runs after the weight prologue's loads are issued: the pointers of
+// gate/up's token rows depend on route positions loaded from memory, and
+// computing them first made every workgroup wait for those loads before it
+// requested any weight (the first block then waited for two memory
+// latencies in a row).  Without it (down: its rows need no load) the
+// prologue interleaves weight and row blocks.
 // after_issue runs once the prologue's loads are in flight (the place for
 // loads whose results are only needed after the stream, e.g. the epilogue's).
 // Weight blocks are loaded DW blocks ahead and token-row blocks DX <= DW
 // ahead (the token rows are L2 hits; the weights come from HBM).
 template <int NT, int MTW, int KS, int NB, int NP, int DW = kDepth, int DX = kDepth,
-          typename Hook = NoHook>
-__device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* const (&xr)[NP],
+          bool kLateX = true, typename MakeXr, typename Hook = NoHook>
+__device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const MakeXr& make_xr,
                                             int slice, bool active, char* smem, char* stage,
                                             sf_f32x4 (&acc)[MTW][NT],
                                             const Hook& after_issue = Hook{}) {
@@ -307,12 +328,26 @@ __device__ __forceinline__ void stream_gemm(const Slab<NT>& w, const uint16_t* c
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
   uint4 wr[DW][2 * NT];
   uint4 xq[DX][MTW][SP];
+  const uint16_t* xr[NP];
+  if constexpr (kLateX) {
 #pragma unroll
-  for (int d = 0; d < DW; ++d) {
-    load_w<NT>(w, d, lane, wave, wr[d]);
-    if (d < DX) {
-      if constexpr (kStaged) load_x_rows(xr, d, xq[d % DX]);
-      else load_x<MTW, SP>(xr, d, s0, xq[d % DX]);
+    for (int d = 0; d < DW; ++d) load_w<NT>(w, d, lane, wave, wr[d]);
+    SF_SCHED_FENCE();
+    make_xr(xr);
+#pragma unroll
+    for (int d = 0; d < DX; ++d) {
+      if constexpr (kStaged) load_x_rows(xr, d, xq[d]);
+      else load_x<MTW, SP>(xr, d, s0, xq[d]);
+    }
+  } else {
+    make_xr(xr);
+#pragma unroll
+    for (int d = 0; d < DW; ++d) {
+      load_w<NT>(w, d, lane, wave, wr[d]);
+      if (d < DX) {
+        if constexpr (kStaged) load_x_rows(xr, d, xq[d]);
+        else load_x<MTW, SP>(xr, d, s0, xq[d]);
+      }
     }
   }
   SF_SCHED_FENCE();
@@ -374,39 +409,52 @@ __device__ __forceinline__ bool reduce_slices(sf_f32x4 (&acc)[1][NT], char* smem
   return q == 0;
 }
 
-// Lane row pointers of a wavefront's A tiles (tile mt*TM + wave%TM of the
-// pass, row 16*tile + l%16 clamped to the pass, + the lane's k offset).  An
-// idle wavefront points every lane at the pass's first row.
-template <int MTW, int TM, typename RowPtr>
-__device__ __forceinline__ bool a_rows(RowPtr row_of, int mp, const uint16_t* (&xr)[MTW]) {
+// A rows of a wavefront, in two steps.  a_fetch issues fetch(row) for the
+// lane's rows (tile mt*TM + wave%TM of the pass, row 16*tile + l%16 clamped
+// to the pass; an idle wavefront takes the pass's first row): for gate/up
+// that loads the route position of the permuted row.  The values are turned
+// into pointers only inside stream_gemm, after its weight prologue is issued
+// (fragment_ptrs: + the lane's k offset; an idle wavefront points every
+// lane at one address).
+template <int MTW, int TM, typename Fetch>
+__device__ __forceinline__ bool a_fetch(Fetch fetch, int mp, int (&pre)[MTW]) {
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const int t0 = wave % TM;
   const bool active = t0 * 16 < mp;
 #pragma unroll
-  for (int mt = 0; mt < MTW; ++mt) {
-    if (active)
-      xr[mt] = row_of(min((mt * TM + t0) * 16 + (lane & 15), mp - 1)) + 8 * (lane >> 4);
-    else
-      xr[mt] = row_of(0);
-  }
+  for (int mt = 0; mt < MTW; ++mt)
+    pre[mt] = fetch(active ? min((mt * TM + t0) * 16 + (lane & 15), mp - 1) : 0);
   return active;
 }
 
-// Row pointers of the staged split: lane l holds rows l/16 + 4i (i < 4) of
-// the wavefront's tile, clamped to the pass, at element 8*(l%16).  An idle
-// wavefront points every lane at the pass's first row.
-template <typename RowPtr>
-__device__ __forceinline__ bool a_rows_staged(RowPtr row_of, int mp, const uint16_t* (&xr)[4]) {
+template <int MTW, typename Ptr>
+__device__ __forceinline__ void fragment_ptrs(Ptr ptr, const int (&pre)[MTW], bool active,
+                                              const uint16_t* (&xr)[MTW]) {
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt) xr[mt] = ptr(pre[mt]) + (active ? 8 * (lane >> 4) : 0);
+}
+
+// Rows of the staged split: lane l holds rows l/16 + 4i (i < 4) of the
+// wavefront's tile, clamped to the pass (an idle wavefront: the pass's first
+// row); its pointers (staged_ptrs) are at element 8*(l%16).
+template <typename Fetch>
+__device__ __forceinline__ bool a_fetch_staged(Fetch fetch, int mp, int (&pre)[4]) {
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int wave = threadIdx.x / SF_WAVE;
   const bool active = wave * 16 < mp;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = active ? min(wave * 16 + (lane >> 4) + 4 * i, mp - 1) : 0;
-    xr[i] = row_of(row) + 8 * (lane & 15);
-  }
+  for (int i = 0; i < 4; ++i) pre[i] = fetch(active ? min(wave * 16 + (lane >> 4) + 4 * i, mp - 1) : 0);
   return active;
+}
+
+template <typename Ptr>
+__device__ __forceinline__ void staged_ptrs(Ptr ptr, const int (&pre)[4],
+                                            const uint16_t* (&xr)[4]) {
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xr[i] = ptr(pre[i]) + 8 * (lane & 15);
 }
 
 // ---------------------------------------------------------------- phase 1 --
@@ -440,17 +488,23 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
   for (int p0 = 0; p0 < wk.m; p0 += kPass) {
     const int mp = min(kPass, wk.m - p0);
     sf_f32x4 acc[MTW][NT];
-    auto row_of = [&](int row) { return row_ptr<R>(a, wk.r0 + p0 + row); };
+    const int base = wk.r0 + p0;
+    auto fetch = [&](int row) { return token_fetch<R>(a, base + row); };
+    auto ptr = [&](int v) { return token_ptr<R>(a, v); };
     if constexpr (KS == 1 && MTW == 1) {
-      const uint16_t* xr[4];
-      const bool active = a_rows_staged(row_of, mp, xr);
-      stream_gemm<NT, MTW, KS, NB, 4, kGateUpDepth>(
-          w, xr, 0, active, smem, smem + 2 * 16 * NT * kRowBytes + wave * kStageBytes, acc);
+      int pre[4];
+      const bool active = a_fetch_staged(fetch, mp, pre);
+      SF_SCHED_FENCE();
+      stream_gemm<NT, MTW, KS, NB, 4, kGateUpDepth, kGateUpDepth>(
+          w, [&](const uint16_t* (&xr)[4]) { staged_ptrs(ptr, pre, xr); }, 0, active, smem,
+          smem + 2 * 16 * NT * kRowBytes + wave * kStageBytes, acc);
     } else {
-      const uint16_t* xr[MTW];
-      const bool active = a_rows<MTW, TM>(row_of, mp, xr);
-      stream_gemm<NT, MTW, KS, NB, MTW, kGateUpDepth>(w, xr, wave / TM, active, smem, nullptr,
-                                                      acc);
+      int pre[MTW];
+      const bool active = a_fetch<MTW, TM>(fetch, mp, pre);
+      SF_SCHED_FENCE();
+      stream_gemm<NT, MTW, KS, NB, MTW, kGateUpDepth, kGateUpDepth>(
+          w, [&](const uint16_t* (&xr)[MTW]) { fragment_ptrs<MTW>(ptr, pre, active, xr); },
+          wave / TM, active, smem, nullptr, acc);
     }
     bool owner = true;
     if constexpr (KS > 1) owner = reduce_slices<NT, KS>(acc, smem);
@@ -481,11 +535,26 @@ __device__ __forceinline__ void gateup_body(const SwigluArgs& a, const ExpertWor
   }
 }
 
+// Waves per SIMD a build must keep at the Qwen3-30B-A3B shape (gate/up 8
+// blocks per row, down 3; list and slot-table launches): the occupancy its
+// tiling was measured at.  Several builds sit a register or two under the
+// limit of their occupancy, so without the floor a small code change could
+// cost each CU a workgroup (gate/up and down of 33..64-row launches hold 3
+// workgroups per CU at <= 168 registers).  Other shapes and the one-expert
+// form take the compiler's choice.
+template <Resolve R, int MC, int NB, int NT>
+constexpr int min_waves() {
+  if (R == Resolve::kDense || (NB != 8 && NB != 3) || MC == 3) return 1;
+  if (NT == 2) return MC == 0 ? 4 : 3;
+  return MC == 0 ? (NB == 8 ? 7 : 5) : 1;
+}
+
 // Row class MC of a build: 0: every expert of the launch has m <= 16, 1:
 // <= 32, 2: <= 64, 3: any.  An expert above its launch's class (max_rows
 // understated) runs in passes of the class's largest split.
 template <Resolve R, int MC, int NB, int NT>
-__global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(const SwigluArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
+    min_waves<R, MC, NB, NT>()))) void gateup_mfma_kernel(const SwigluArgs a) {
   __shared__ __attribute__((aligned(16)))
   char smem[2 * 16 * NT * kRowBytes + (MC >= 2 ? kWaves * kStageBytes : 0)];
   const int tiles = a.I / (8 * NT);
@@ -521,9 +590,15 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
   w.stride = I;
   for (int p0 = 0; p0 < wk.m; p0 += kPass) {
     const int mp = min(kPass, wk.m - p0);
+    int pre[MTW];
+    const bool active = a_fetch<MTW, TM>([&](int row) { return wk.r0 + p0 + row; }, mp, pre);
     const uint16_t* ar[MTW];
-    const bool active = a_rows<MTW, TM>(
-        [&](int row) { return a.act + static_cast<int64_t>(wk.r0 + p0 + row) * I; }, mp, ar);
+    fragment_ptrs<MTW>([&](int r) { return a.act + static_cast<int64_t>(r) * I; }, pre, active,
+                       ar);
+    auto act_rows = [&](const uint16_t* (&xr)[MTW]) {
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) xr[mt] = ar[mt];
+    };
     // Routing weights of this lane's output rows.  The epilogue used to
     // read perm_pos and then route_w for each row after the stream (two
     // dependent global latencies per row at the end of a short workgroup);
@@ -544,8 +619,8 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
     SF_SCHED_FENCE();
     sf_f32x4 acc[MTW][NT];
     stream_gemm<NT, MTW, KS, NB, MTW, (NB < kDownDepth ? NB : kDownDepth),
-                (KS == 4 && NB >= kDownDepth ? kDownDepth : kDepth)>(
-        w, ar, wave / TM, active, smem, nullptr, acc, [&] {
+                (KS == 4 && NB >= kDownDepth ? kDownDepth : kDepth), false>(
+        w, act_rows, wave / TM, active, smem, nullptr, acc, [&] {
           if (scaled) {
 #pragma unroll
             for (int mt = 0; mt < MTW; ++mt)
@@ -576,7 +651,8 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
 }
 
 template <Resolve R, int MC, int NB, int NT>
-__global__ __launch_bounds__(kThreads) void down_mfma_kernel(const SwigluArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
+    min_waves<R, MC, NB, NT>()))) void down_mfma_kernel(const SwigluArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[2 * 16 * NT * kRowBytes];
   const int tiles = a.H / (16 * NT);
   const int j = blockIdx.x / tiles;
