@@ -35,6 +35,8 @@
  *                        (eagle3_types.py:450-473); each Qwen3 attention layer
  *                        then calls transformers sdpa_attention_forward
  *                        (integrations/sdpa_attention.py) with that mask
+ *   sf_rms_norm          tf:294-299  Qwen3MoeRMSNorm.forward (the four norms
+ *                        of every decoder layer of the verification forward)
  */
 #ifndef SPECFIT_AMD_H
 #define SPECFIT_AMD_H
@@ -46,7 +48,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 8
+#define SF_ABI_VERSION 9
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -274,6 +276,21 @@ int sf_tree_attention(const void *q, int64_t q_stride_token,
                       int64_t mask_stride_query, int queries, int keys,
                       int q_heads, int kv_heads, int head_dim, float scale,
                       void *out, sf_stream_t stream);
+
+/*
+ * K6: RMSNorm over the last dimension.  Replaces Qwen3MoeRMSNorm.forward
+ * (tf:294-299):
+ *   v = mean over d of float(x[r, d])^2 (fp32)
+ *   out[r, d] = bf16(float(weight[d]) * bf16(float(x[r, d]) * rsqrt(v + eps)))
+ *   x       bf16, row r at x + r * row_stride (elements), dim elements
+ *   weight  bf16 [dim]
+ *   out     bf16, row r at out + r * out_stride (may equal x: in place)
+ * The fp32 sum of squares runs in a fixed order of its own, so results can
+ * differ from the eager module by a last-place rounding of the variance.
+ */
+int sf_rms_norm(const void *x, int64_t row_stride, int rows, int dim,
+                const void *weight, float eps, void *out, int64_t out_stride,
+                sf_stream_t stream);
 
 #ifdef __cplusplus
 }

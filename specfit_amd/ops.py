@@ -635,3 +635,32 @@ def tree_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
             handle)
         _native.check(rc, "sf_tree_attention")
     return out
+
+
+# ------------------------------------------------------------------ K6 ----
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *,
+             stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """RMSNorm over the last dimension (K6): bf16(weight * bf16(x * rsqrt(
+    mean(x^2) + eps))) with the mean in fp32, as Qwen3MoeRMSNorm.forward.
+    ``x`` is bf16 with a unit last stride and rows at a uniform stride (a
+    contiguous tensor, or a view such as [..., heads, head_dim] of one);
+    returns a new contiguous tensor of x's shape."""
+    _require_cuda("x", x, _BF16)
+    _require_cuda("weight", weight, _BF16)
+    dim = x.shape[-1]
+    if weight.dim() != 1 or weight.shape[0] != dim or weight.stride(0) != 1:
+        raise ValueError(f"weight must be a contiguous bf16 [{dim}] tensor")
+    if x.dim() == 0:
+        raise ValueError("x must have at least one dimension")
+    out = torch.empty(x.shape, dtype=_BF16, device=x.device)
+    rows = out.numel() // dim if dim else 0
+    if rows == 0:
+        return out
+    flat = x.reshape(rows, dim)  # a view whenever the rows share one stride
+    if flat.stride(1) != 1:
+        flat = flat.contiguous()
+    rc = _native.lib().sf_rms_norm(flat.data_ptr(), flat.stride(0), rows, dim, weight.data_ptr(),
+                                   float(eps), out.data_ptr(), dim,
+                                   _stream_handle(stream, x.device))
+    _native.check(rc, "sf_rms_norm")
+    return out

@@ -150,6 +150,7 @@ class _Transfer:
     generation: int
     submission_sequence: int
     ready_event: torch.cuda.Event
+    stream: int | None = None  # raw handle of the copy stream (None: unknown)
 
 
 class _SourceOwner(Protocol):
@@ -847,7 +848,8 @@ class GpuExpertCache:
         slot.ready_event = ready
         slot.write_stream = stream
         slot.ready_seq = self._submission_sequence
-        transfer = _Transfer(key, slot.slot_id, slot.generation, self._submission_sequence, ready)
+        transfer = _Transfer(key, slot.slot_id, slot.generation, self._submission_sequence, ready,
+                             int(stream.cuda_stream))
         self._inflight[key] = transfer
         self._outstanding_transfers.append(transfer)
         self._stats.h2d_submissions += 1
@@ -877,12 +879,22 @@ class GpuExpertCache:
         stream.wait_event(guard)
 
     def _reap_completed_transfers(self) -> None:
-        """Publish completed transfers as resident, in submission order."""
+        """Publish completed transfers as resident, in submission order.
+        When the oldest one has completed, the newest transfer of each copy
+        stream in the queue is queried: if all of those completed, so did
+        every transfer (each stream completes its copies in order), and the
+        queue is published without querying each event."""
         queue = self._outstanding_transfers
         if not queue or not queue[0].ready_event.query():
             return
         slots, resident, inflight = self._slots, self._resident, self._inflight
-        while queue and queue[0].ready_event.query():
+        if len(queue) > 2 and self._newest_per_stream_done(queue):
+            done = len(queue)
+        else:
+            done = 1
+            while done < len(queue) and queue[done].ready_event.query():
+                done += 1
+        for _ in range(done):
             t = queue.popleft()
             slot = slots[t.slot_id]
             if slot.generation == t.generation and slot.expert_id == t.expert_id:
@@ -890,6 +902,18 @@ class GpuExpertCache:
             if inflight.get(t.expert_id) == t:
                 del inflight[t.expert_id]
         self._state_version += 1
+
+    @staticmethod
+    def _newest_per_stream_done(queue) -> bool:
+        seen = set()
+        for t in reversed(queue):
+            if t.stream is None:
+                return False
+            if t.stream not in seen:
+                if not t.ready_event.query():
+                    return False
+                seen.add(t.stream)
+        return True
 
     def _reap_completed_use_guards(self) -> None:
         reaped = False

@@ -1,0 +1,98 @@
+"""K6 (sf_rms_norm) against transformers' Qwen3MoeRMSNorm and a float64
+evaluation of the same formula (tf:294-299).  The kernel sums the squares
+in its own fp32 order, so its output may differ from the eager module's by
+the rounding of the variance.  That moves the first bf16 rounding by at
+most one step, which the weight multiply and the second rounding can turn
+into two: the tests bound the difference to two bf16 steps and require
+nearly every element to be bitwise equal."""
+import math
+
+import pytest
+import torch
+
+from specfit_amd import ops
+from specfit_amd.runtime import Qwen3RMSNormHip, install_hip_norms
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_steps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """|a - b| in units of the bf16 spacing at b (elementwise)."""
+    a, b = a.float(), b.float()
+    exp = torch.floor(torch.log2(b.abs().clamp_min(2.0 ** -126)))
+    return (a - b).abs() / torch.exp2(exp - 7)
+
+
+def _reference_f64(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """The eager formula with the variance in float64, then the module's two
+    bf16 rounding points."""
+    xf = x.double()
+    var = xf.pow(2).mean(-1, keepdim=True)
+    y = (xf * torch.rsqrt(var + eps)).to(torch.bfloat16)
+    return (w.double() * y.double()).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("shape", [(61, 2048), (1, 61, 32, 128), (1, 61, 4, 128), (3, 4096),
+                                   (7, 24), (5, 40), (2, 8, 13)])
+def test_rms_norm_matches_the_eager_module(device, shape):
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeRMSNorm
+
+    torch.manual_seed(sum(shape))
+    dim = shape[-1]
+    x = (torch.randn(shape, device=device) * 3).to(torch.bfloat16)
+    eager = Qwen3MoeRMSNorm(dim, eps=1e-6).to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        eager.weight.copy_((1 + 0.1 * torch.randn(dim, device=device)).to(torch.bfloat16))
+    hip = Qwen3RMSNormHip.from_module(eager)
+    with torch.no_grad():
+        expected = eager(x)
+        actual = hip(x)
+    torch.cuda.synchronize()
+    assert actual.shape == expected.shape and actual.dtype == torch.bfloat16
+    steps = _bf16_steps(actual, expected)
+    exact = (actual == expected).float().mean().item()
+    print(f"{shape}: {exact:.4%} bitwise equal to the eager module, "
+          f"max {steps.max().item():.0f} bf16 steps", flush=True)
+    assert steps.max().item() <= 2.0, shape
+    assert exact >= 0.98
+    ref = _reference_f64(x, eager.weight, 1e-6)
+    assert _bf16_steps(actual, ref).max().item() <= 2.0
+
+
+def test_rms_norm_of_strided_views_and_empty_inputs(device):
+    torch.manual_seed(3)
+    w = torch.randn(128, device=device).to(torch.bfloat16)
+    base = torch.randn(61, 4096, device=device).to(torch.bfloat16)
+    view = base.view(1, 61, 32, 128)
+    assert torch.equal(ops.rms_norm(view, w, 1e-6), ops.rms_norm(view.contiguous(), w, 1e-6))
+    # rows at a non-contiguous stride: every other row of the matrix
+    rows = base[::2, :128]
+    assert torch.equal(ops.rms_norm(rows, w, 1e-6), ops.rms_norm(rows.contiguous(), w, 1e-6))
+    empty = torch.empty(0, 128, dtype=torch.bfloat16, device=device)
+    assert ops.rms_norm(empty, w, 1e-6).shape == (0, 128)
+    with pytest.raises(ValueError):
+        ops.rms_norm(base, w, 1e-6)  # weight of the wrong length
+
+
+def test_installing_hip_norms_keeps_the_model_output(device):
+    """The Qwen3-MoE dense path with its norms on K6 stays within bf16
+    rounding of the eager norms (experts replaced by identity to isolate
+    the norms)."""
+    from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
+
+    torch.manual_seed(7)
+    cfg = Qwen3MoeConfig(vocab_size=128, hidden_size=256, intermediate_size=256,
+                         moe_intermediate_size=64, num_hidden_layers=2, num_attention_heads=4,
+                         num_key_value_heads=2, head_dim=64, num_experts=4,
+                         num_experts_per_tok=2, max_position_embeddings=64)
+    model = Qwen3MoeForCausalLM(cfg).to(device=device, dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, 128, (1, 12), device=device)
+    with torch.no_grad():
+        expected = model(ids).logits.float()
+        replaced = install_hip_norms(model)
+        actual = model(ids).logits.float()
+    assert replaced == 2 * 4 + 1  # four per decoder layer and the final norm
+    assert isinstance(model.model.norm, Qwen3RMSNormHip)
+    err = (actual - expected).abs().max().item() / expected.abs().max().item()
+    assert err < 2e-2, err
+    assert not math.isnan(err)
