@@ -894,13 +894,21 @@ class GpuExpertCache:
             done = 1
             while done < len(queue) and queue[done].ready_event.query():
                 done += 1
+        # A _ResidentMap takes one version for the whole batch (below).
+        batched = type(resident) is _ResidentMap
+        publish = dict.__setitem__ if batched else type(resident).__setitem__
         for _ in range(done):
             t = queue.popleft()
+            key = t.expert_id
             slot = slots[t.slot_id]
-            if slot.generation == t.generation and slot.expert_id == t.expert_id:
-                resident[t.expert_id] = t.slot_id
-            if inflight.get(t.expert_id) == t:
-                del inflight[t.expert_id]
+            held = slot.expert_id
+            if slot.generation == t.generation and (held is key or held == key):
+                publish(resident, key, t.slot_id)
+            current = inflight.get(key)
+            if current is t or (current is not None and current == t):
+                del inflight[key]
+        if batched:
+            resident.version = next(_versions)
         self._state_version += 1
 
     @staticmethod

@@ -173,7 +173,8 @@ class Qwen3OffloadedExperts(nn.Module):
             return self._forward_prefetched(hidden_states, top_k_index, top_k_weights)
         if execution_order is None and self._uses_slot_table():
             return self._forward_slot_table(hidden_states, top_k_index, top_k_weights)
-        routes, active = self._prepare(hidden_states, top_k_index, top_k_weights)
+        routes, active = self._prepare(hidden_states, top_k_index, top_k_weights,
+                                       idle=self._reap_while_routing)
         order = self._resolve_execution_order(active, execution_order)
         if routes is None:
             return torch.zeros_like(hidden_states)
@@ -338,6 +339,16 @@ class Qwen3OffloadedExperts(nn.Module):
         counts = self._read_counts(plan, top_k_index, num_experts, idle)
         active = tuple(compress(range(num_experts), counts))
         return routes, active
+
+    def _reap_while_routing(self) -> bool:
+        """While the counts are on their way: publish the transfers that
+        complete meanwhile (the previous forward's last copies), work the
+        execution order would otherwise do after the counts arrive.  True
+        while transfers are outstanding."""
+        cache = self.cache
+        with cache._lock:
+            cache._reap_completed_transfers()
+            return bool(cache._outstanding_transfers)
 
     def _counts_staging(self, num_experts: int) -> torch.Tensor:
         if self._host_counts is None:
