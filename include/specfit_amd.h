@@ -37,6 +37,9 @@
  *                        (integrations/sdpa_attention.py) with that mask
  *   sf_rms_norm          tf:294-299  Qwen3MoeRMSNorm.forward (the four norms
  *                        of every decoder layer of the verification forward)
+ *   sf_qk_norm_rope      tf:162-167  the query/key norms and
+ *                        apply_rotary_pos_emb (tf:58-81) of
+ *                        Qwen3MoeAttention.forward
  */
 #ifndef SPECFIT_AMD_H
 #define SPECFIT_AMD_H
@@ -291,6 +294,27 @@ int sf_tree_attention(const void *q, int64_t q_stride_token,
 int sf_rms_norm(const void *x, int64_t row_stride, int rows, int dim,
                 const void *weight, float eps, void *out, int64_t out_stride,
                 sf_stream_t stream);
+
+/*
+ * K7: query/key RMSNorm and rotary embedding of one attention layer (batch
+ * 1).  Replaces, in Qwen3MoeAttention.forward (tf:162-167),
+ * q_norm(q.view(T, Hq, D)), k_norm(k.view(T, Hk, D)) and
+ * apply_rotary_pos_emb (tf:58-81):
+ *   n = sf_rms_norm's row result (same bits)
+ *   out[h, t, d] = bf16(bf16(n[d] * cos[t, d]) + bf16(rot(n)[d] * sin[t, d]))
+ *   rot(n)[d] = -n[d + D/2] for d < D/2, n[d - D/2] otherwise
+ *   q, k        bf16 [tokens, q_heads | kv_heads, head_dim], contiguous
+ *   q_weight, k_weight  bf16 [head_dim]
+ *   cos, sin    bf16 [tokens, head_dim], contiguous
+ *   q_out, k_out  bf16 [q_heads | kv_heads, tokens, head_dim], contiguous
+ * head_dim must be 128 (SF_ERR_UNSUPPORTED_SHAPE otherwise); all buffers
+ * 16-byte aligned.
+ */
+int sf_qk_norm_rope(const void *q, const void *k, int tokens, int q_heads,
+                    int kv_heads, int head_dim, const void *q_weight,
+                    const void *k_weight, float eps, const void *cos,
+                    const void *sin, void *q_out, void *k_out,
+                    sf_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,7 @@ SIGNATURES = {
     "sf_tree_attention": ([_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64,
                            _i, _i, _i, _i, _i, ctypes.c_float, _p, _p], _i),
     "sf_rms_norm": ([_p, _i64, _i, _i, _p, ctypes.c_float, _p, _i64, _p], _i),
+    "sf_qk_norm_rope": ([_p, _p, _i, _i, _i, _i, _p, _p, ctypes.c_float, _p, _p, _p, _p, _p], _i),
 }
 
 

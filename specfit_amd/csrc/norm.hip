@@ -120,3 +120,112 @@ extern "C" int sf_rms_norm(const void* x, int64_t row_stride, int rows, int dim,
   SF_LAUNCH_CHECK();
   return SF_OK;
 }
+
+// ------------------------------------------------------------------ K7 ----
+// Query/key RMSNorm and rotary embedding of one attention layer, fused.
+// Restates, for head_dim 128 and batch 1,
+//   q = q_norm(q_proj(h).view(T, Hq, D)), k = k_norm(k_proj(h).view(T, Hk, D))
+//   (Qwen3MoeAttention.forward, tf:162-163) and apply_rotary_pos_emb
+//   (tf:58-81) with rotate_half (tf:51-55):
+//   x_embed[d] = bf16(bf16(x[d] * cos[t, d]) + bf16(rot(x)[d] * sin[t, d])),
+//   rot(x)[d] = -x[d + 64] for d < 64, x[d - 64] otherwise,
+// where x is the normed row.  Each eager operation rounds to bf16, so the
+// fused form reproduces them exactly; the norm is K6's (same lane layout and
+// summation order, so the same bits).  The eager form is twelve kernels per
+// layer (two norms, then per tensor a negation, a concatenation, two
+// products and a sum).
+//
+// A row (one token's head) is 16 lanes x 8 elements; a wavefront takes four
+// rows, so the norm's sum is the 16-lane butterfly K6 applies to a
+// 128-element row, and the rotation partner of lane j's elements (d +- 64)
+// sits in lane j ^ 8 of the same 16-lane row (one DPP row rotation).
+// Outputs are written head-major: out[h][t][d].
+namespace {
+
+constexpr int kRopeDim = 128;
+
+__device__ __forceinline__ float row16_sum(float x) {
+  x += sf_dpp<0xB1>(x);   // lane ^ 1
+  x += sf_dpp<0x4E>(x);   // lane ^ 2
+  x += sf_dpp<0x141>(x);  // row_half_mirror
+  x += sf_dpp<0x140>(x);  // row_mirror
+  return x;
+}
+
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, int tokens, int q_heads,
+    int kv_heads, const uint16_t* __restrict__ wq, const uint16_t* __restrict__ wk, float eps,
+    const uint16_t* __restrict__ cos, const uint16_t* __restrict__ sin,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out) {
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+  const int j = lane & 15;
+  const int q_rows = tokens * q_heads;
+  const int rows = q_rows + tokens * kv_heads;
+  const int row = (blockIdx.x * kThreads + threadIdx.x) / 16;
+  // Rows past the end repeat the last row's loads (no store): the DPP moves
+  // below need every lane of the 16-lane row active.
+  const bool live = row < rows;
+  const int r = live ? row : rows - 1;
+  const bool is_q = r < q_rows;
+  const int rr = is_q ? r : r - q_rows;
+  const int heads = is_q ? q_heads : kv_heads;
+  const int t = rr / heads;
+  const int h = rr - t * heads;
+  const uint16_t* src = (is_q ? q : k) + static_cast<int64_t>(rr) * kRopeDim;
+  const uint16_t* w = is_q ? wq : wk;
+  float f[8], g[8], c[8], s[8];
+  unpack(ld16(src + 8 * j), f);
+  unpack(ld16(w + 8 * j), g);
+  unpack(ld16(cos + static_cast<int64_t>(t) * kRopeDim + 8 * j), c);
+  unpack(ld16(sin + static_cast<int64_t>(t) * kRopeDim + 8 * j), s);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+  const float var = row16_sum(ss) * (1.0f / static_cast<float>(kRopeDim));
+  const float rs = __builtin_amdgcn_rsqf(var + eps);
+  float n[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) n[i] = sf_round_bf16(g[i] * sf_round_bf16(f[i] * rs));
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    float e[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float partner = sf_dpp<0x128>(n[i + u]);  // row_ror 8: lane j ^ 8
+      const float rot = j < 8 ? -partner : partner;
+      e[u] = sf_round_bf16(sf_round_bf16(n[i + u] * c[i + u]) + sf_round_bf16(rot * s[i + u]));
+    }
+    o[i / 2] = static_cast<uint32_t>(sf_f32_to_bf16(e[0])) |
+               (static_cast<uint32_t>(sf_f32_to_bf16(e[1])) << 16);
+  }
+  if (live) {
+    uint16_t* dst = (is_q ? q_out : k_out) +
+                    (static_cast<int64_t>(h) * tokens + t) * kRopeDim + 8 * j;
+    *reinterpret_cast<uint4*>(dst) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+}  // namespace
+
+extern "C" int sf_qk_norm_rope(const void* q, const void* k, int tokens, int q_heads,
+                               int kv_heads, int head_dim, const void* q_weight,
+                               const void* k_weight, float eps, const void* cos, const void* sin,
+                               void* q_out, void* k_out, sf_stream_t stream) {
+  if (tokens < 0 || q_heads < 1 || kv_heads < 1 || !(eps >= 0.f)) return SF_ERR_INVALID_ARGUMENT;
+  if (head_dim != kRopeDim) return SF_ERR_UNSUPPORTED_SHAPE;
+  if (tokens == 0) return SF_OK;
+  const void* ptrs[] = {q, k, q_weight, k_weight, cos, sin, q_out, k_out};
+  for (const void* p : ptrs)
+    if (!p || !aligned16(p)) return SF_ERR_INVALID_ARGUMENT;
+  const long long rows = static_cast<long long>(tokens) * (q_heads + kv_heads);
+  if (rows > 0x7fffffffLL / 16) return SF_ERR_UNSUPPORTED_SHAPE;
+  const unsigned blocks = static_cast<unsigned>((rows * 16 + kThreads - 1) / kThreads);
+  qk_norm_rope_kernel<<<dim3(blocks), dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), tokens, q_heads, kv_heads,
+      static_cast<const uint16_t*>(q_weight), static_cast<const uint16_t*>(k_weight), eps,
+      static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
+      static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out));
+  SF_LAUNCH_CHECK();
+  return SF_OK;
+}

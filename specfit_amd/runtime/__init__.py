@@ -11,6 +11,7 @@ from .qwen3_offloaded_experts import (ExpertExecutionPolicy, Qwen3OffloadedExper
 from .qwen3_expert_prefetch import Qwen3ExpertPrefetch
 from .qwen3_offloaded_model import (LoadedOffloadedQwen3, PackedExpertBackingMode,
                                     Qwen3LoadTimings, build_offloaded_qwen3, load_offloaded_qwen3)
+from .qwen3_attention import Qwen3AttentionHip, install_hip_attention
 from .qwen3_norm import Qwen3RMSNormHip, install_hip_norms
 from .qwen3_router import Qwen3MoeTopKRouterHip
 from .replay import (ExpertAccessReplayResult, LogicalReplayError, LogicalReplayEvent,
@@ -28,7 +29,7 @@ __all__ = [
     "ExpertLease", "GpuExpertCache", "GpuExpertCacheSnapshot", "NoEvictableSlotError",
     "LoadedOffloadedQwen3", "PackedExpertBackingMode", "PendingTransferSnapshot", "Qwen3ExpertPrefetch", "Qwen3LoadTimings",
     "Qwen3MoeTopKRouterHip", "Qwen3OffloadedExperts", "Qwen3RMSNormHip", "build_offloaded_qwen3",
-    "install_hip_norms",
+    "install_hip_norms", "Qwen3AttentionHip", "install_hip_attention",
     "load_offloaded_qwen3",
     "RecordingCacheTransitionObserver", "ReductionMode", "RuntimeEventKind",
     "aggregate_cache_transition_counters",

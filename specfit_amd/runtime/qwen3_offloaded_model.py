@@ -30,6 +30,7 @@ from .cache_observer import CacheTransitionObserver
 from .gpu_expert_cache import GpuExpertCache
 from .lease import ExpertCacheStats
 from .qwen3_offloaded_experts import ExpertExecutionPolicy, Qwen3OffloadedExperts, ReductionMode
+from .qwen3_attention import install_hip_attention
 from .qwen3_norm import install_hip_norms
 from .qwen3_router import Qwen3MoeTopKRouterHip
 from .state import ExpertKey
@@ -235,8 +236,10 @@ def _install(model, *, layer_packed: dict[int, torch.Tensor], device: torch.devi
                 intermediate_size=config.moe_intermediate_size, reduction_mode=reduction_mode,
                 execution_policy=expert_execution_policy, h2d_prefetch=h2d_prefetch)
             layer.mlp.gate = Qwen3MoeTopKRouterHip.from_module(layer.mlp.gate)
-        # The dense layers' RMSNorms run as one kernel each (K6).
+        # The dense layers' RMSNorms run as one kernel each (K6), and each
+        # attention layer's query/key norms and rotary embedding as one (K7).
         install_hip_norms(model)
+        install_hip_attention(model)
     except BaseException:
         for cache in reversed(caches):
             cache.close()

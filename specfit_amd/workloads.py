@@ -131,7 +131,7 @@ def make_verify_model(*, device, layers: int = 48, slots_per_layer: int = 12, se
             else:
                 p.normal_(0.0, std, generator=gen)
     model.to(torch.bfloat16)
-    model.model.rotary_emb = Qwen3MoeRotaryEmbedding(config, device=device)
+    model.model.rotary_emb = Qwen3MoeRotaryEmbedding(config).to(device)
     if experts is None:
         experts = make_layer(seed=seed, pin_memory=True)
     return build_offloaded_qwen3(model, device=device, slots_per_layer=slots_per_layer,

@@ -96,3 +96,75 @@ def test_installing_hip_norms_keeps_the_model_output(device):
     err = (actual - expected).abs().max().item() / expected.abs().max().item()
     assert err < 2e-2, err
     assert not math.isnan(err)
+
+
+def _attention_config(head_dim):
+    from transformers import Qwen3MoeConfig
+
+    return Qwen3MoeConfig(vocab_size=128, hidden_size=256, intermediate_size=256,
+                          moe_intermediate_size=64, num_hidden_layers=1, num_attention_heads=4,
+                          num_key_value_heads=2, head_dim=head_dim, num_experts=4,
+                          num_experts_per_tok=2, max_position_embeddings=256,
+                          attn_implementation="sdpa")
+
+
+@pytest.mark.parametrize("tokens", [1, 7, 61, 128])
+def test_qk_norm_rope_equals_the_eager_sequence_bitwise(device, tokens):
+    """K7 against the eager sequence of Qwen3MoeAttention.forward (tf:162-167)
+    with the norms on K6: q_norm/k_norm, transpose, apply_rotary_pos_emb."""
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import (Qwen3MoeRotaryEmbedding,
+                                                                    apply_rotary_pos_emb)
+
+    torch.manual_seed(tokens)
+    Hq, Hk, D = 32, 4, 128
+    q = (torch.randn(1, tokens, Hq, D, device=device) * 2).to(torch.bfloat16)
+    k = (torch.randn(1, tokens, Hk, D, device=device) * 2).to(torch.bfloat16)
+    wq = (1 + 0.2 * torch.randn(D, device=device)).to(torch.bfloat16)
+    wk = (1 + 0.2 * torch.randn(D, device=device)).to(torch.bfloat16)
+    cfg = _attention_config(D)
+    rope = Qwen3MoeRotaryEmbedding(cfg).to(device)
+    positions = (1000 + torch.arange(tokens, device=device)).unsqueeze(0)
+    cos, sin = rope(q, positions)
+    qn = Qwen3RMSNormHip(torch.nn.Parameter(wq), 1e-6)
+    kn = Qwen3RMSNormHip(torch.nn.Parameter(wk), 1e-6)
+    eq, ek = apply_rotary_pos_emb(qn(q).transpose(1, 2), kn(k).transpose(1, 2), cos, sin)
+    aq, ak = ops.qk_norm_rope(q, k, wq, wk, 1e-6, cos, sin)
+    assert aq.shape == (1, Hq, tokens, D) and ak.shape == (1, Hk, tokens, D)
+    assert torch.equal(aq, eq) and torch.equal(ak, ek)
+
+
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_hip_attention_module_matches_the_hf_module(device, head_dim):
+    """Qwen3AttentionHip (fused at head_dim 128, eager norms+rotary at 64)
+    gives the HF module's output bit for bit when both use K6 norms."""
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import (Qwen3MoeAttention,
+                                                                    Qwen3MoeRotaryEmbedding)
+
+    from specfit_amd.runtime import Qwen3AttentionHip
+
+    torch.manual_seed(head_dim)
+    cfg = _attention_config(head_dim)
+    hf = Qwen3MoeAttention(cfg, layer_idx=0).to(device=device, dtype=torch.bfloat16).eval()
+    with torch.no_grad():
+        for norm in (hf.q_norm, hf.k_norm):
+            norm.weight.copy_((1 + 0.2 * torch.randn(head_dim, device=device)).to(torch.bfloat16))
+    hf.q_norm = Qwen3RMSNormHip.from_module(hf.q_norm)
+    hf.k_norm = Qwen3RMSNormHip.from_module(hf.k_norm)
+    hip = Qwen3AttentionHip.from_module(hf)
+    T = 12
+    h = torch.randn(1, T, 256, device=device).to(torch.bfloat16)
+    pos = torch.arange(T, device=device).unsqueeze(0)
+    emb = Qwen3MoeRotaryEmbedding(cfg).to(device)(h, pos)
+    mask = torch.tril(torch.ones(T, T, dtype=torch.bool, device=device)).view(1, 1, T, T)
+    with torch.no_grad():
+        expected, _ = hf(h, emb, mask)
+        actual, _ = hip(h, emb, mask)
+    assert torch.equal(actual, expected)
+
+
+def test_qk_norm_rope_rejects_other_head_dims(device):
+    q = torch.zeros(1, 2, 4, 64, dtype=torch.bfloat16, device=device)
+    w = torch.ones(64, dtype=torch.bfloat16, device=device)
+    cs = torch.zeros(1, 2, 64, dtype=torch.bfloat16, device=device)
+    with pytest.raises(RuntimeError, match="unsupported"):
+        ops.qk_norm_rope(q, q, w, w, 1e-6, cs, cs)
