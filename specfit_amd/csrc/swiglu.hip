@@ -165,6 +165,10 @@ constexpr int kSteps = kBlockK / 32;  // MFMA k-steps per block
 // listed experts).  Measured slower elsewhere: gate/up at 3 (83.7 -> 85.5
 // us), and down's wider splits at 3 (64-token all-resident down 33.9 -> 39.3
 // us: their A fragments of a third block cost registers).
+// Down's two-tile split (experts above 64 rows) loads its activation rows
+// one block ahead instead: with two A tiles per wavefront a second block of
+// them held 238 registers, one workgroup per CU; at one block ahead it holds
+// 174, two per CU (launches of 12-48 such experts: down 15-29% faster).
 constexpr int kDepth = 2;
 constexpr int kDownDepth = 3;
 constexpr int kGateUpDepth = 2;  // 4 measured no faster (class 1 at 84 experts 6% slower)
@@ -619,7 +623,7 @@ __device__ __forceinline__ void down_body(const SwigluArgs& a, const ExpertWork&
     SF_SCHED_FENCE();
     sf_f32x4 acc[MTW][NT];
     stream_gemm<NT, MTW, KS, NB, MTW, (NB < kDownDepth ? NB : kDownDepth),
-                (KS == 4 && NB >= kDownDepth ? kDownDepth : kDepth), false>(
+                (KS == 4 && NB >= kDownDepth ? kDownDepth : (MTW == 2 ? 1 : kDepth)), false>(
         w, act_rows, wave / TM, active, smem, nullptr, acc, [&] {
           if (scaled) {
 #pragma unroll
