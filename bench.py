@@ -69,6 +69,14 @@ def parse_args():
     p.add_argument("--tree-nodes", type=int, default=60)
     p.add_argument("--tree-depth", type=int, default=6)
     p.add_argument("--verify-slots", type=int, default=12)
+    p.add_argument("--expert-sets", type=int, default=24,
+                   help="48-layer forwards: distinct pinned expert sets (1.125 GiB each); layer l "
+                        "copies its misses from set l mod N.  The GPU boxes this was measured on "
+                        "cap page-locked memory at ~36 GiB per process, so 48 distinct sets "
+                        "(54 GiB) do not fit")
+    p.add_argument("--shared-experts", action="store_true",
+                   help="48-layer forwards: every layer's cache copies from one layer's pinned "
+                        "experts, drawn on the host as in the single-layer workloads")
     p.add_argument("--executor", choices=("layer", "ready_demand", "predicted"), default="layer",
                    help="48-layer forwards only. layer: each MoE layer's own resident-first, "
                         "one-ahead sequence; ready_demand: the predicted-prefetch scheduler "
@@ -203,13 +211,25 @@ def main_verify(args) -> int:
 
     from specfit_amd import ops
     from specfit_amd.runtime import synthetic_tree, verify_draft_tree
-    from specfit_amd.workloads import make_kv_context, make_layer, make_verify_model
+    from specfit_amd.workloads import (make_kv_context, make_layer, make_layer_sources,
+                                       make_verify_model)
 
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
-    experts = make_layer(seed=0, pin_memory=True)
-    loaded = make_verify_model(device=dev, layers=args.layers, slots_per_layer=args.verify_slots,
-                               experts=experts)
+    if args.shared_experts:
+        experts = make_layer(seed=0, pin_memory=True)
+        expert_bytes = experts.expert_bytes
+        loaded = make_verify_model(device=dev, layers=args.layers,
+                                   slots_per_layer=args.verify_slots, experts=experts)
+    else:
+        n_src = min(args.layers, args.expert_sets)
+        sources = make_layer_sources(n_src, device=dev, seed=0)
+        expert_bytes = sources[0].shape[1] * sources[0].element_size()
+        log(f"{n_src} distinct pinned expert sets drawn in {time.perf_counter() - t0:.1f}s "
+            f"({sum(s.numel() for s in sources) * 2 / 2**30:.1f} GiB)")
+        loaded = make_verify_model(device=dev, layers=args.layers,
+                                   slots_per_layer=args.verify_slots,
+                                   layer_sources=[sources[l % n_src] for l in range(args.layers)])
     target = loaded.model
     config = target.config
     cache = make_kv_context(config, args.context, device=dev, seed=1)
@@ -305,7 +325,6 @@ def main_verify(args) -> int:
         if recorded:
             with ops.record_launches(copies=True, park_cycles=PARK_CYCLES) as rec:
                 rec_wall, rec_misses, _, _ = run_steps(args.warmup + args.steps, rec)
-    expert_bytes = experts.expert_bytes
     H = config.hidden_size
     k3 = [(nx, rows, tag, s_.elapsed_time(e_) * 1e-3) for nx, rows, tag, s_, e_ in rec.k3]
     k3_time = sum(x[3] for x in k3)
@@ -327,8 +346,11 @@ def main_verify(args) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: random-init N(0,0.02) bf16 weights (one layer's 128 experts shared by "
-                "every layer's cache), random N(0,1) 1024-token KV context, seeded random trees",
+        "data": ("synthetic: random-init N(0,0.02) bf16 weights ("
+                 + ("one layer's 128 experts shared by every layer's cache" if args.shared_experts
+                    else f"{min(args.layers, args.expert_sets)} distinct pinned expert sets, layer "
+                         f"l copies from set l mod {min(args.layers, args.expert_sets)}")
+                 + f"), random N(0,1) {args.context}-token KV context, seeded random trees"),
         "config": {"workload": (f"qwen3-30b-a3b verification forward, {args.layers} layers, "
                                 f"{args.tree_nodes}-node depth-{args.tree_depth} tree over a "
                                 f"{args.context}-token context, {args.verify_slots}-slot LRU expert "

@@ -72,6 +72,30 @@ def make_layer(*, seed: int = 0, hidden_size: int = 2048, num_experts: int = 128
     return MoELayerWeights(router, experts, H, I, top_k, bias)
 
 
+def make_layer_sources(layers: int, *, device, seed: int = 0, hidden_size: int = 2048,
+                       num_experts: int = 128, intermediate_size: int = 768,
+                       std: float = 0.02) -> list[torch.Tensor]:
+    """Distinct packed experts for each of ``layers`` MoE layers, in page-locked
+    host memory: bf16 [E, 3*I*H] N(0, std) per layer (1.125 GiB at the
+    Qwen3-30B-A3B shape), drawn on ``device`` from a generator seeded with
+    seed + layer and copied to the host one expert block at a time."""
+    device = torch.device(device)
+    E, row = num_experts, 3 * intermediate_size * hidden_size
+    chunk = 16  # experts per device draw: 302 MB of fp32 at the 30B shape
+    out = []
+    for layer in range(layers):
+        gen = torch.Generator(device=device).manual_seed(seed + layer)
+        host = torch.empty((E, row), dtype=torch.bfloat16, pin_memory=True)
+        for e0 in range(0, E, chunk):
+            n = min(chunk, E - e0)
+            block = torch.empty((n, row), dtype=torch.float32, device=device)
+            block.normal_(0.0, std, generator=gen)
+            host[e0:e0 + n].copy_(block.to(torch.bfloat16))
+        out.append(host)
+    torch.cuda.synchronize(device)
+    return out
+
+
 def make_hidden(tokens: int, hidden_size: int = 2048, *, seed: int,
                 zipf_fold: bool = False) -> torch.Tensor:
     """bf16 [tokens, hidden] ~ N(0, 1); feature 0 := 1 when the Zipf bias is
@@ -99,15 +123,17 @@ QWEN3_30B_A3B_MODEL = dict(vocab_size=151936, hidden_size=2048, intermediate_siz
 
 def make_verify_model(*, device, layers: int = 48, slots_per_layer: int = 12, seed: int = 0,
                       experts: MoELayerWeights | None = None, std: float = 0.02,
-                      expert_execution_policy: str = "resident_first"):
+                      expert_execution_policy: str = "resident_first",
+                      layer_sources: list[torch.Tensor] | None = None):
     """A Qwen3-30B-A3B-shaped target for the verification forward, random
     init: every non-expert weight N(0, std) bf16 (norm weights 1), drawn on
-    the device from a seeded generator; the routed experts of every layer
-    are the pinned packed experts of ``experts`` (one MoE layer's worth,
-    shared by all layers so the host holds 1.2 GB instead of 58 GB; every
-    layer still has its own slot cache and copies its own misses).  The
-    attention layers run the HIP tree-attention kernel.  Returns the
-    LoadedOffloadedQwen3."""
+    the device from a seeded generator.  The routed experts of layer l are
+    ``layer_sources[l]`` (distinct pinned packed experts per layer, see
+    make_layer_sources) or, without them, the pinned packed experts of
+    ``experts`` (one MoE layer's worth shared by all layers, so the host
+    holds 1.2 GB instead of 54 GB; every layer still has its own slot cache
+    and copies its own misses).  The attention layers run the HIP
+    tree-attention kernel.  Returns the LoadedOffloadedQwen3."""
     from accelerate import init_empty_weights
     from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
     from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeRotaryEmbedding
@@ -132,10 +158,16 @@ def make_verify_model(*, device, layers: int = 48, slots_per_layer: int = 12, se
                 p.normal_(0.0, std, generator=gen)
     model.to(torch.bfloat16)
     model.model.rotary_emb = Qwen3MoeRotaryEmbedding(config).to(device)
-    if experts is None:
-        experts = make_layer(seed=seed, pin_memory=True)
+    if layer_sources is not None:
+        if len(layer_sources) != layers:
+            raise ValueError("layer_sources needs one tensor per layer")
+        sources = {l: layer_sources[l] for l in range(layers)}
+    else:
+        if experts is None:
+            experts = make_layer(seed=seed, pin_memory=True)
+        sources = {l: experts.experts for l in range(layers)}
     return build_offloaded_qwen3(model, device=device, slots_per_layer=slots_per_layer,
-                                 layer_experts={l: experts.experts for l in range(layers)},
+                                 layer_experts=sources,
                                  expert_execution_policy=expert_execution_policy)
 
 

@@ -55,6 +55,7 @@ def test_bench_48_layer_forward_under_the_prefetch_scheduler(device, workload, e
     assert len(lines) == 1, out.stdout[-2000:]
     d = json.loads(lines[0])
     assert d["value"] > 0 and d["config"]["executor"] == executor and d["config"]["layers"] == 2
+    assert "2 distinct pinned expert sets" in d["data"]
     s = d["scheduler"]
     assert s["complete"] and 1 <= s["peak_inflight"] <= s["max_inflight"] == 2
     per = s["per_forward"]
