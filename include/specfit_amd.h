@@ -29,6 +29,8 @@
  *                        (index_add_ in canonical or arrival order)
  *   sf_copy_h2d          src/specfit/runtime/gpu_expert_cache.py:556-561
  *                        (slot.tensor.copy_(pinned_source, non_blocking=True))
+ *   sf_expert_decode     the same copy when the transfer moves an
+ *                        exponent-coded record (decoded into the slot)
  *   sf_tree_attention    the attention of the verification forward:
  *                        eagle3_tree.py:1202-1240 runs the target with
  *                        Eagle3DraftTree.verification_attention_mask
@@ -51,7 +53,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 9
+#define SF_ABI_VERSION 10
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -253,6 +255,32 @@ int sf_combine(const void *rows, const int64_t *topk_index,
  */
 int sf_copy_h2d(void *device_dst, const void *host_src, size_t bytes,
                 sf_stream_t stream);
+
+/*
+ * Exponent-coded expert records: the host-to-device transfer of an expert
+ * may move a lossless record of its bf16 weights instead of the raw bytes
+ * (about 75% of them for weights that span at most 15 binary exponents),
+ * decoded into the slot on the device.  Together with sf_copy_h2d of the
+ * record into a staging buffer this replaces the same
+ * slot.tensor.copy_(pinned_source) (gpu_expert_cache.py:556-561); the slot
+ * ends with the same bytes.  Record of n bf16 values with e escapes (every
+ * section 256-byte aligned):
+ *   S  [n] uint8            sign << 7 | mantissa of value i
+ *   X  [ceil(n/2)] uint8    4-bit code of value i in byte i/2 (even i: low
+ *                           nibble); code c < 15: exponent exponent_table[c];
+ *                           code 15: an escape
+ *   EI [e] uint32           ascending indices of the escaped values
+ *   EE [e] uint8            their exponent bytes
+ * sf_expert_record_bytes returns the record size (-1 for invalid counts).
+ * sf_expert_decode writes out[i] = sign | exponent | mantissa of value i:
+ *   record          device buffer of at least record_bytes >= the record size
+ *   exponent_table  host array of 16 exponent bytes (entry 15 is unused)
+ *   out             bf16 [n_values], 16-byte aligned like record
+ */
+int64_t sf_expert_record_bytes(int64_t n_values, int64_t n_escapes);
+int sf_expert_decode(const void *record, size_t record_bytes, int64_t n_values,
+                     const uint8_t *exponent_table, int n_escapes, void *out,
+                     sf_stream_t stream);
 
 /*
  * K5: grouped-query attention of the verification forward over the cached

@@ -19,7 +19,7 @@ LIB_PATH = os.path.join(LIB_DIR, "libspecfit_amd.so")
 OFFLOAD_ARCH = "gfx950"
 
 SOURCES = ("abi.hip", "router.hip", "dispatch.hip", "swiglu.hip", "combine.hip",
-           "attention.hip", "norm.hip")
+           "attention.hip", "norm.hip", "codec.hip")
 
 HIPCC_FLAGS = (
     f"--offload-arch={OFFLOAD_ARCH}",

@@ -591,6 +591,23 @@ def copy_h2d(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) ->
     _native.check(rc, "sf_copy_h2d")
 
 
+def expert_decode(record: torch.Tensor, n_escapes: int, table: bytes, out: torch.Tensor,
+                  stream: torch.cuda.Stream | None = None) -> None:
+    """out (bf16, on the device) <- the values of an exponent-coded expert
+    record (uint8, on the device; layout in specfit_amd.codec)."""
+    _require_cuda("record", record, torch.uint8)
+    _require_cuda("out", out, _BF16)
+    if record.dim() != 1 or not record.is_contiguous() or not out.is_contiguous():
+        raise ValueError("expert_decode needs a contiguous 1-D record and a contiguous output")
+    if len(table) != 16:
+        raise ValueError("the exponent table has 16 entries")
+    tbl = (ctypes.c_uint8 * 16).from_buffer_copy(bytes(table))
+    rc = _native.lib().sf_expert_decode(_ptr(record), record.numel(), out.numel(), tbl,
+                                        int(n_escapes), _ptr(out),
+                                        _stream_handle(stream, out.device))
+    _native.check(rc, "sf_expert_decode")
+
+
 # ------------------------------------------------------------------ K5 ----
 def tree_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                    mask: torch.Tensor | None, scale: float, *,

@@ -48,6 +48,7 @@ from typing import Hashable, Mapping, Protocol, Sequence
 import torch
 
 from .. import ops
+from ..codec import CompressedExperts
 from . import lease as _lease_mod
 from .cache_observer import CacheTransitionObserver
 from .cache_snapshot import CacheSlotSnapshot, GpuExpertCacheSnapshot, PendingTransferSnapshot
@@ -238,11 +239,16 @@ class GpuExpertCache:
                  cache_id: str | None = None, queue_id: str | None = None,
                  observer: CacheTransitionObserver | None = None,
                  source_owner: _SourceOwner | None = None,
-                 copy_streams: tuple[torch.cuda.Stream, torch.cuda.Stream] | None = None) -> None:
+                 copy_streams: tuple[torch.cuda.Stream, torch.cuda.Stream] | None = None,
+                 compressed_sources: CompressedExperts | None = None) -> None:
         """``copy_streams``: two SDMA streams the cache's transfers alternate
         between, instead of a pair of its own.  The layer caches of one
         model share a pair (layers copy one after another; per-cache pairs
-        of 48 layers ran at ~89% of the link rate one shared pair reaches)."""
+        of 48 layers ran at ~89% of the link rate one shared pair reaches).
+        ``compressed_sources``: exponent-coded records of (some of) the
+        experts (specfit_amd.codec); their transfers move the record into
+        a device staging buffer and decode it into the slot, which then
+        holds the same bytes as a raw copy of the source."""
         if not cpu_sources:
             raise ValueError("cpu_sources must contain at least one expert")
         if slot_count <= 0:
@@ -265,6 +271,13 @@ class GpuExpertCache:
 
         self._sources, self._source_order = _stage_sources(
             cpu_sources, adopt_pinned_sources, source_owner is not None)
+        if compressed_sources is not None:
+            if not isinstance(compressed_sources, CompressedExperts):
+                raise ValueError("compressed_sources must be a CompressedExperts image")
+            if compressed_sources.numel != next(iter(self._sources.values())).numel():
+                raise ValueError("compressed_sources do not match the experts' size")
+            if any(key not in self._sources for key in compressed_sources.records):
+                raise ValueError("compressed_sources hold an expert the cache does not know")
         # Each source key maps to itself: slots and maps hold these objects,
         # so lookups with them match by identity.
         self._key_objects = {key: key for key in self._sources}
@@ -278,6 +291,10 @@ class GpuExpertCache:
             self._own_copy_stream = self.copy_stream
             self._storage = torch.empty((slot_count, *first.shape), dtype=first.dtype,
                                         device=self.device)
+            # Two staging buffers for coded transfers (by submission parity).
+            staging = compressed_sources.staging_bytes() if compressed_sources else 0
+            self._staging = [torch.empty(staging, dtype=torch.uint8, device=self.device)
+                             for _ in range(2 if staging else 0)]
             # The allocation may be recycled memory that kernels queued on the
             # current stream still read: order the first copies after them.
             here = torch.cuda.current_stream(self.device)
@@ -304,6 +321,10 @@ class GpuExpertCache:
         self._lock = RLock()
         # (keys, resident-map version, table) of the last _slot_table.
         self._table_memo: tuple | None = None
+        self._codec = compressed_sources
+        # (event, stream) after the decode that last read each staging buffer
+        self._staging_reader: list = [None, None]
+        self.h2d_bytes = 0  # bytes moved over the host link
 
     # ------------------------------------------------------------- queries --
     @property
@@ -773,6 +794,9 @@ class GpuExpertCache:
             self._forget_assignments()
             self._sources.clear()
             self._key_objects.clear()
+            self._codec = None
+            self._staging = []
+            self._staging_reader = [None, None]
             owner, self._source_owner = self._source_owner, None
             if owner is not None:
                 owner.close()
@@ -842,9 +866,11 @@ class GpuExpertCache:
             stream.wait_event(slot.ready_event)
         for guard in readers:
             self._await_reader(stream, guard)
-        ops.copy_h2d(slot.tensor, self._sources[key], stream)
+        staged = self._copy_in(slot, key, stream)
         ready = torch.cuda.Event(blocking=False)
         ready.record(stream)
+        if staged is not None:
+            self._staging_reader[staged] = (ready, stream)
         slot.ready_event = ready
         slot.write_stream = stream
         slot.ready_seq = self._submission_sequence
@@ -860,6 +886,26 @@ class GpuExpertCache:
             self._record_transition(_K.H2D_SUBMIT, key, slot,
                                     submission_sequence=transfer.submission_sequence,
                                     ready_event=ready)
+
+    def _copy_in(self, slot: _Slot, key: Hashable, stream: torch.cuda.Stream) -> int | None:
+        """Enqueue the expert's H2D into the slot on ``stream``: the raw
+        bytes, or its record into a staging buffer plus the decode into the
+        slot.  Returns the staging buffer used (None: raw copy)."""
+        codec = self._codec
+        rec = codec.records.get(key) if codec is not None else None
+        if rec is None or rec.raw:
+            ops.copy_h2d(slot.tensor, self._sources[key], stream)
+            self.h2d_bytes += slot.tensor.numel() * slot.tensor.element_size()
+            return None
+        j = self._submission_sequence & 1
+        last = self._staging_reader[j]
+        if last is not None and last[1] is not stream:
+            stream.wait_event(last[0])  # the previous decode out of this buffer
+        buf = self._staging[j][:rec.nbytes]
+        ops.copy_h2d(buf, codec.blob[rec.offset:rec.offset + rec.nbytes], stream)
+        ops.expert_decode(buf, rec.n_escapes, rec.table, slot.tensor, stream)
+        self.h2d_bytes += rec.nbytes
+        return j
 
     @staticmethod
     def _await_reader(stream: torch.cuda.Stream, guard: torch.cuda.Event) -> None:

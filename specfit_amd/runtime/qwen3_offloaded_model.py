@@ -26,6 +26,7 @@ from pathlib import Path
 
 import torch
 
+from ..codec import CompressedExperts
 from .cache_observer import CacheTransitionObserver
 from .gpu_expert_cache import GpuExpertCache
 from .lease import ExpertCacheStats
@@ -217,19 +218,29 @@ def _pack_layer_experts(get, names: dict, E: int, H: int, I: int) -> torch.Tenso
 
 def _install(model, *, layer_packed: dict[int, torch.Tensor], device: torch.device,
              slots_per_layer: int, reduction_mode, expert_execution_policy,
-             h2d_prefetch: bool, cache_observer) -> tuple:
+             h2d_prefetch: bool, cache_observer, compress_expert_sources: bool = False) -> tuple:
     config = model.config
     caches = []
     # One pair of SDMA streams for every layer cache (layers copy in turn).
     copy_streams = (torch.cuda.Stream(device=device), torch.cuda.Stream(device=device))
+    coded: dict[int, CompressedExperts] = {}  # layers sharing a source share its records
     try:
         for layer_id, layer in enumerate(model.model.layers):
             packed = layer_packed[layer_id]
-            cache = GpuExpertCache({ExpertKey(layer_id, e): packed[e] for e in range(packed.shape[0])},
+            sources = {ExpertKey(layer_id, e): packed[e] for e in range(packed.shape[0])}
+            image = None
+            if compress_expert_sources:
+                shared = coded.get(id(packed))
+                if shared is None:
+                    shared = coded[id(packed)] = CompressedExperts.encode(
+                        {e: packed[e] for e in range(packed.shape[0])}, device=device)
+                image = CompressedExperts(shared.blob, {ExpertKey(layer_id, e): r for e, r
+                                                        in shared.records.items()}, shared.numel)
+            cache = GpuExpertCache(sources,
                                    slot_count=slots_per_layer, device=device,
                                    adopt_pinned_sources=True, cache_id=f"qwen3-layer-{layer_id}",
                                    queue_id=f"layer-{layer_id}-copy", observer=cache_observer,
-                                   copy_streams=copy_streams)
+                                   copy_streams=copy_streams, compressed_sources=image)
             caches.append(cache)
             layer.mlp.experts = Qwen3OffloadedExperts(
                 layer_id=layer_id, cache=cache, hidden_size=config.hidden_size,
@@ -255,13 +266,17 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
                          expert_execution_policy=ExpertExecutionPolicy.EXPERT_ID_ASCENDING,
                          attn_implementation: str = "sdpa",
                          cache_observer: CacheTransitionObserver | None = None,
-                         h2d_prefetch: bool = True) -> LoadedOffloadedQwen3:
+                         h2d_prefetch: bool = True,
+                         compress_expert_sources: bool = False) -> LoadedOffloadedQwen3:
     """Load a Qwen3-MoE checkpoint with offloaded experts
     (qwen3_offloaded_model.py:667-840).  ``model_root`` holds config.json
     and the original safetensors (per-expert or fused expert tensors); with
     ``packed_checkpoint_root`` the experts and non-experts come from that
     packed-v1 checkpoint instead, validated against ``model_root``'s
-    config/index hashes (the weight shards need not exist)."""
+    config/index hashes (the weight shards need not exist).
+    ``compress_expert_sources`` (an extension of this build): every layer's
+    misses move exponent-coded records (specfit_amd.codec) over the host
+    link and are decoded into the slots, which hold the same bytes."""
     from accelerate import init_empty_weights
     from safetensors import safe_open
     from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
@@ -375,7 +390,8 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
     caches = _install(model, layer_packed=layer_packed, device=device,
                       slots_per_layer=slots_per_layer, reduction_mode=reduction_mode,
                       expert_execution_policy=policy, h2d_prefetch=h2d_prefetch,
-                      cache_observer=cache_observer)
+                      cache_observer=cache_observer,
+                      compress_expert_sources=compress_expert_sources)
     t["expert_cache_initialization_seconds"] = time.perf_counter() - t5
     t6 = time.perf_counter()
     meta = [n for n, p in model.named_parameters() if p.is_meta]
@@ -400,7 +416,8 @@ def build_offloaded_qwen3(model, *, device, slots_per_layer: int,
                           expert_execution_policy=ExpertExecutionPolicy.EXPERT_ID_ASCENDING,
                           cache_observer: CacheTransitionObserver | None = None,
                           h2d_prefetch: bool = True,
-                          layer_experts: dict[int, torch.Tensor] | None = None
+                          layer_experts: dict[int, torch.Tensor] | None = None,
+                          compress_expert_sources: bool = False
                           ) -> LoadedOffloadedQwen3:
     """Offload the experts of an in-memory HF ``Qwen3MoeForCausalLM``.
 
@@ -428,7 +445,8 @@ def build_offloaded_qwen3(model, *, device, slots_per_layer: int,
     caches = _install(model, layer_packed=packed, device=device, slots_per_layer=slots_per_layer,
                       reduction_mode=reduction_mode,
                       expert_execution_policy=ExpertExecutionPolicy(expert_execution_policy),
-                      h2d_prefetch=h2d_prefetch, cache_observer=cache_observer)
+                      h2d_prefetch=h2d_prefetch, cache_observer=cache_observer,
+                      compress_expert_sources=compress_expert_sources)
     model.requires_grad_(False)
     model.eval()
     return LoadedOffloadedQwen3(model=model, expert_caches=caches, load_timings=None)

@@ -1,0 +1,142 @@
+"""Exponent-coded expert transfers on the device.
+
+The decode kernel (sf_expert_decode) must restore every value's bits: a
+decoded buffer is compared byte for byte with the raw bf16 values, at the
+Qwen3-30B-A3B expert size, over every bf16 bit pattern (escape-heavy records
+forced) and around the 4096-value chunk edges.  A cache fed by coded records
+must then behave as the raw cache: identical slot bytes, counters and layer
+outputs over the same request sequence, at the 64-token, 24-slot Zipf
+layer of the headline benchmark.
+"""
+import pytest
+import torch
+
+from specfit_amd import ops
+from specfit_amd.codec import CompressedExperts, encode_record
+from specfit_amd.runtime import (ExpertKey, GpuExpertCache, Qwen3MoeTopKRouterHip,
+                                 Qwen3OffloadedExperts)
+from specfit_amd.workloads import make_hidden, make_layer_sources, zipf_bias
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K = 2048, 768, 128, 8
+
+
+def _decode(values: torch.Tensor, force: bool = False) -> torch.Tensor:
+    rec, n_esc, table = encode_record(values, force=force)
+    assert rec is not None
+    out = torch.full_like(values, float("nan"))
+    ops.expert_decode(rec, n_esc, table, out)
+    torch.cuda.synchronize()
+    return out
+
+
+def _same_bits(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_decode_restores_an_expert_at_the_real_size(device):
+    g = torch.Generator(device=device).manual_seed(0)
+    values = (torch.randn(3 * I * H, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    rec, n_esc, _ = encode_record(values)
+    print(f"expert record: {rec.numel()} of {2 * values.numel()} bytes, {n_esc} escapes",
+          flush=True)
+    assert rec.numel() <= 0.751 * 2 * values.numel()
+    assert _same_bits(_decode(values), values)
+
+
+def test_decode_every_bit_pattern(device):
+    values = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16)
+    values = values.view(torch.bfloat16)
+    assert _same_bits(_decode(values, force=True), values)
+
+
+@pytest.mark.parametrize("n", [1, 15, 4096, 4097, 3 * 4096 + 17])
+def test_decode_chunk_edges_and_tails(device, n):
+    g = torch.Generator(device=device).manual_seed(n)
+    values = (torch.randn(n, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    # escapes on both sides of every chunk edge and at the ends
+    rare = torch.tensor([3.0e38, -1.0e-30, 0.0, float("inf")], device=device).to(torch.bfloat16)
+    for j, pos in enumerate({0, n - 1, *[p for c in range(4096, n, 4096) for p in (c - 1, c)]}):
+        values[pos] = rare[j % rare.numel()]
+    assert _same_bits(_decode(values, force=True), values)
+
+
+def test_decode_rejects_short_or_misaligned_records(device):
+    values = torch.ones(4096, dtype=torch.bfloat16, device=device)
+    rec, n_esc, table = encode_record(values, force=True)
+    out = torch.empty_like(values)
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        ops.expert_decode(rec[:-256], n_esc, table, out)
+    shifted = torch.zeros(rec.numel() + 16, dtype=torch.uint8, device=device)
+    shifted[1:1 + rec.numel()] = rec
+    with pytest.raises(RuntimeError, match="misaligned"):
+        ops.expert_decode(shifted[1:], n_esc, table, out)
+
+
+@pytest.fixture(scope="module")
+def zipf_sources(device):
+    packed = make_layer_sources(1, device=device, seed=11)[0]
+    g = torch.Generator().manual_seed(0)
+    router = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    router[:, 0] = zipf_bias(E, 1.1, 1.0, 7919).to(torch.bfloat16)
+    image = CompressedExperts.encode({ExpertKey(0, e): packed[e] for e in range(E)},
+                                     device=device)
+    return packed, router, image
+
+
+def _layer(device, packed, router_w, slots, image=None):
+    router = Qwen3MoeTopKRouterHip(num_experts=E, hidden_size=H, top_k=K, norm_topk_prob=True,
+                                   device=device)
+    with torch.no_grad():
+        router.weight.copy_(router_w)
+    cache = GpuExpertCache({ExpertKey(0, e): packed[e] for e in range(E)}, slot_count=slots,
+                           device=device, adopt_pinned_sources=True, compressed_sources=image)
+    experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H, intermediate_size=I,
+                                    execution_policy="resident_first", h2d_prefetch=True)
+    return router, cache, experts
+
+
+def test_coded_cache_matches_the_raw_cache(device, zipf_sources):
+    """64-token Zipf steps through a 24-slot layer: the coded cache gives the
+    same outputs, counters and slot bytes as the raw one, with ~75% of the
+    bytes over the link."""
+    packed, router_w, image = zipf_sources
+    assert image.transfer_bytes <= 0.751 * image.raw_bytes
+    runs = []
+    for coded in (False, True):
+        router, cache, experts = _layer(device, packed, router_w, 24, image if coded else None)
+        outs = []
+        for step in range(6):
+            h = make_hidden(64, seed=500 + step, zipf_fold=True).to(device)
+            _, w, idx = router(h)
+            outs.append(experts(h, idx, w))
+        torch.cuda.synchronize()
+        runs.append((outs, cache.stats(), cache.storage.clone(), cache.h2d_bytes,
+                     cache.resident_expert_ids()))
+        cache.close()
+    (o_raw, s_raw, st_raw, b_raw, r_raw), (o_cod, s_cod, st_cod, b_cod, r_cod) = runs
+    print(f"coded cache: {s_cod.h2d_submissions} transfers, {b_cod} of {b_raw} bytes", flush=True)
+    assert s_raw == s_cod and r_raw == r_cod and s_raw.h2d_submissions > 24
+    assert all(torch.equal(a, b) for a, b in zip(o_raw, o_cod))
+    assert _same_bits(st_raw, st_cod)
+    assert b_cod < 0.76 * b_raw
+
+
+def test_coded_cache_under_copy_stream_switches(device, zipf_sources):
+    """A cache whose transfers all go to one replaced copy stream (as under
+    the prefetch scheduler) and back: staging reuse is ordered across the
+    streams and every slot ends with its expert's bytes."""
+    packed, router_w, image = zipf_sources
+    cache = GpuExpertCache({ExpertKey(0, e): packed[e] for e in range(E)}, slot_count=4,
+                           device=device, adopt_pinned_sources=True, compressed_sources=image)
+    other = torch.cuda.Stream(device=device)
+    own = cache.copy_stream
+    for i, e in enumerate([3, 9, 27, 81, 5, 6, 7, 3, 100, 101]):
+        cache.copy_stream = other if i % 3 == 1 else own
+        with cache.acquire(ExpertKey(0, e)) as lease:
+            got = lease.wait().clone()
+        torch.cuda.synchronize()
+        assert _same_bits(got, packed[e].to(device)), f"expert {e}"
+    cache.copy_stream = own
+    cache.close()
