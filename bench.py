@@ -69,6 +69,10 @@ def parse_args():
     p.add_argument("--tree-nodes", type=int, default=60)
     p.add_argument("--tree-depth", type=int, default=6)
     p.add_argument("--verify-slots", type=int, default=12)
+    p.add_argument("--transfer", choices=("raw", "coded"), default="coded",
+                   help="what a miss moves over the host link: the expert's exponent-coded "
+                        "record (specfit_amd.codec, ~75%% of the bytes, decoded into the slot "
+                        "on the device; the slot holds the same bytes), or its raw bf16 bytes")
     p.add_argument("--expert-sets", type=int, default=24,
                    help="48-layer forwards: distinct pinned expert sets (1.125 GiB each); layer l "
                         "copies its misses from set l mod N.  The GPU boxes this was measured on "
@@ -216,20 +220,26 @@ def main_verify(args) -> int:
 
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
+    coded = args.transfer == "coded"
     if args.shared_experts:
         experts = make_layer(seed=0, pin_memory=True)
         expert_bytes = experts.expert_bytes
         loaded = make_verify_model(device=dev, layers=args.layers,
-                                   slots_per_layer=args.verify_slots, experts=experts)
+                                   slots_per_layer=args.verify_slots, experts=experts,
+                                   compress_expert_sources=coded)
     else:
         n_src = min(args.layers, args.expert_sets)
-        sources = make_layer_sources(n_src, device=dev, seed=0)
+        # Coded transfers copy from the page-locked records only, so the raw
+        # sets can stay in pageable memory.
+        sources = make_layer_sources(n_src, device=dev, seed=0, pin_memory=not coded)
         expert_bytes = sources[0].shape[1] * sources[0].element_size()
-        log(f"{n_src} distinct pinned expert sets drawn in {time.perf_counter() - t0:.1f}s "
-            f"({sum(s.numel() for s in sources) * 2 / 2**30:.1f} GiB)")
+        log(f"{n_src} distinct expert sets drawn in {time.perf_counter() - t0:.1f}s "
+            f"({sum(s.numel() for s in sources) * 2 / 2**30:.1f} GiB"
+            f"{', pageable' if coded else ' pinned'})")
         loaded = make_verify_model(device=dev, layers=args.layers,
                                    slots_per_layer=args.verify_slots,
-                                   layer_sources=[sources[l % n_src] for l in range(args.layers)])
+                                   layer_sources=[sources[l % n_src] for l in range(args.layers)],
+                                   compress_expert_sources=coded)
     target = loaded.model
     config = target.config
     cache = make_kv_context(config, args.context, device=dev, seed=1)
@@ -348,7 +358,8 @@ def main_verify(args) -> int:
         "dtype": "bf16",
         "data": ("synthetic: random-init N(0,0.02) bf16 weights ("
                  + ("one layer's 128 experts shared by every layer's cache" if args.shared_experts
-                    else f"{min(args.layers, args.expert_sets)} distinct pinned expert sets, layer "
+                    else f"{min(args.layers, args.expert_sets)} distinct expert sets "
+                         f"({'their coded records' if coded else 'raw'} in pinned memory), layer "
                          f"l copies from set l mod {min(args.layers, args.expert_sets)}")
                  + f"), random N(0,1) {args.context}-token KV context, seeded random trees"),
         "config": {"workload": (f"qwen3-30b-a3b verification forward, {args.layers} layers, "
@@ -360,7 +371,7 @@ def main_verify(args) -> int:
                    "tree_depth": args.tree_depth, "cache_slots": args.verify_slots,
                    "attention": "HIP tree attention (K5)",
                    "execution_policy": "resident_first", "h2d_prefetch": True,
-                   "executor": executor},
+                   "executor": executor, "transfer": args.transfer},
         "per_layer_tokens_per_s": value * args.layers,
         "roofline": {"bound": "hbm", "achieved": k3_achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": k3_achieved / HBM_PEAK_GBS, "traffic": None,
@@ -369,7 +380,9 @@ def main_verify(args) -> int:
         "cpu_baseline": None,
         "recorded_ms_per_step": rec_wall / args.steps * 1e3 if rec_wall else None,
         "device_ms_per_step": step_stats(step_events),
-        "h2d": {"achieved_gbs": rec_misses * expert_bytes / h2d_time / 1e9 if h2d_time else None,
+        "h2d": {"achieved_gbs": rec.h2d_bytes / h2d_time / 1e9 if h2d_time else None,
+                "expert_gbs": rec_misses * expert_bytes / h2d_time / 1e9 if h2d_time else None,
+                "transfer": args.transfer,
                 "transfers": rec_misses, "busy_ms": h2d_time * 1e3,
                 "link_busy_frac": h2d_time / rec_wall if h2d_time else None},
         "cache": {"misses_per_layer": misses / (args.steps * args.layers),
@@ -413,9 +426,16 @@ def main_sweep(args) -> int:
         router.weight.copy_(layer.router)
     points = []
     slots = 12
+    image = None
+    if args.transfer == "coded":
+        from specfit_amd.codec import CompressedExperts
+
+        image = CompressedExperts.encode({ExpertKey(0, e): layer.experts[e] for e in range(E)},
+                                         device=dev)
     for T in (1, 8, 32, 64, 128):
         cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(E)},
-                               slot_count=slots, device=dev, adopt_pinned_sources=True)
+                               slot_count=slots, device=dev, adopt_pinned_sources=True,
+                               compressed_sources=image)
         experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H,
                                         intermediate_size=I, execution_policy="resident_first",
                                         h2d_prefetch=True)
@@ -484,7 +504,9 @@ def main_sweep(args) -> int:
             "k3_flop_per_weight_byte": k3_flops / k3_weight if k3_weight else None,
             "k3_gbs": k3_bytes / k3_time / 1e9 if k3_time else None,
             "k3_frac": k3_bytes / k3_time / 1e9 / HBM_PEAK_GBS if k3_time else None,
-            "h2d_gbs": rec_misses * layer.expert_bytes / h2d_time / 1e9 if h2d_time else None,
+            "h2d_gbs": rec.h2d_bytes / h2d_time / 1e9 if h2d_time else None,
+            "h2d_expert_gbs": (rec_misses * layer.expert_bytes / h2d_time / 1e9
+                               if h2d_time else None),
             "h2d_link_busy_frac": h2d_time / rec_wall if h2d_time else None,
         })
         log(f"T={T}: {points[-1]['tokens_per_s']:.0f} tokens/s, "
@@ -495,7 +517,8 @@ def main_sweep(args) -> int:
             "higher_is_better": True, "dtype": "bf16", "data": "synthetic (as the layer workload)",
             "config": {"workload": "qwen3-30b-a3b moe layer, 12-slot LRU cache, zipf 1.1, "
                                    "prewarm 32 cycles, tokens 1/8/32/64/128",
-                       "cache_slots": slots, "prewarm_cycles": args.prewarm},
+                       "cache_slots": slots, "prewarm_cycles": args.prewarm,
+                       "transfer": args.transfer},
             "points": points}
     print(json.dumps(line), flush=True)
     return 0
@@ -520,6 +543,7 @@ def main() -> int:
     import torch
 
     from specfit_amd import ops
+    from specfit_amd.codec import CompressedExperts
     from specfit_amd.runtime import (ExpertKey, GpuExpertCache, Qwen3MoeTopKRouterHip,
                                      Qwen3OffloadedExperts)
     from specfit_amd.workloads import make_hidden, make_layer
@@ -541,9 +565,16 @@ def main() -> int:
                                    device=dev)
     with torch.no_grad():
         router.weight.copy_(layer.router)
+    image = None
+    if args.transfer == "coded":
+        t1 = time.perf_counter()
+        image = CompressedExperts.encode({ExpertKey(0, e): layer.experts[e] for e in range(E)},
+                                         device=dev)
+        log(f"experts coded in {time.perf_counter() - t1:.1f}s: {image.transfer_bytes} of "
+            f"{image.raw_bytes} B ({image.transfer_bytes / image.raw_bytes:.4f})")
     cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(E)}, slot_count=slots,
                            device=dev, adopt_pinned_sources=True, cache_id="qwen3-layer-0",
-                           queue_id="layer-0-copy")
+                           queue_id="layer-0-copy", compressed_sources=image)
     experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H, intermediate_size=I,
                                     execution_policy="resident_first", h2d_prefetch=True)
 
@@ -620,7 +651,8 @@ def main() -> int:
     res = [x for x in k3 if x[2] == "resident"]
     res_bytes = sum(k3_bytes(n, r) for n, r, _, _ in res)
     res_time = sum(x[3] for x in res)
-    h2d_bytes = rec_misses * expert_bytes
+    h2d_bytes = rec.h2d_bytes  # bytes over the link (coded records or raw experts)
+    h2d_expert_bytes = rec_misses * expert_bytes
     h2d_time = rec.copy_busy_seconds() if rec.windows else 0.0
     # Overlap of transfers and expert GEMMs: (t_h2d + t_gemm - t_union) /
     # min(t_h2d, t_gemm), with t_union the measured union of the copy windows
@@ -718,7 +750,8 @@ def main() -> int:
                                 f"prewarm {args.prewarm} cycles"),
                    "tokens": T, "hidden": H, "experts": E, "top_k": K, "intermediate": I,
                    "cache_slots": slots, "prewarm_cycles": args.prewarm,
-                   "execution_policy": "resident_first", "h2d_prefetch": True},
+                   "execution_policy": "resident_first", "h2d_prefetch": True,
+                   "transfer": args.transfer},
         "record": args.record,
         "recorded_ms_per_step": rec_wall / args.steps * 1e3 if rec_wall else None,
         "device_ms_per_step": step_stats(step_events),
@@ -731,7 +764,10 @@ def main() -> int:
                      "alg_bytes_per_launch": k3_alg / max(len(k3), 1)},
         "cpu_baseline": cpu,
         "h2d": {"achieved_gbs": h2d_bytes / h2d_time / 1e9 if h2d_time else None,
+                "expert_gbs": h2d_expert_bytes / h2d_time / 1e9 if h2d_time else None,
+                "transfer": args.transfer,
                 "link_peak_gbs": best, "transfers": rec_misses, "bytes": h2d_bytes,
+                "expert_bytes": h2d_expert_bytes,
                 "busy_ms": h2d_time * 1e3,
                 "note": "busy = union over steps of [first copy start, last copy end] on the two "
                         "copy streams"},

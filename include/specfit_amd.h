@@ -68,6 +68,8 @@ extern "C" {
 #define SF_MAX_EXPERTS 256
 /* Largest top-k. */
 #define SF_MAX_TOPK 32
+/* Values per chunk of an exponent-coded expert record (sf_expert_decode). */
+#define SF_DECODE_CHUNK 4096
 
 typedef void *sf_stream_t;
 
@@ -271,6 +273,8 @@ int sf_copy_h2d(void *device_dst, const void *host_src, size_t bytes,
  *                           code 15: an escape
  *   EI [e] uint32           ascending indices of the escaped values
  *   EE [e] uint8            their exponent bytes
+ *   EC [c + 1] uint32       EC[k] = number of escapes below value
+ *                           k * SF_DECODE_CHUNK (c = ceil(n / SF_DECODE_CHUNK))
  * sf_expert_record_bytes returns the record size (-1 for invalid counts).
  * sf_expert_decode writes out[i] = sign | exponent | mantissa of value i:
  *   record          device buffer of at least record_bytes >= the record size

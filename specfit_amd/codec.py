@@ -16,8 +16,8 @@ An expert whose record would not be smaller stays raw.
 
 Record layout (``sf_expert_record_bytes`` / include/specfit_amd.h): S
 [n] uint8, X [ceil(n/2)] uint8 (value i's code in byte i/2, low nibble for
-even i), EI [e] uint32 ascending, EE [e] uint8; each section 256-byte
-aligned.
+even i), EI [e] uint32 ascending, EE [e] uint8, EC [ceil(n/4096) + 1]
+uint32 (EC[k] = escapes below value 4096 k); each section 256-byte aligned.
 """
 from __future__ import annotations
 
@@ -28,6 +28,7 @@ import torch
 
 ESCAPE = 15           # the code of a value whose exponent is not in the table
 TABLE_SIZE = 15       # exponents a table holds
+CHUNK = 4096          # values per entry of the chunk table (SF_DECODE_CHUNK)
 _ALIGN = 256
 
 
@@ -40,15 +41,17 @@ def record_bytes(n_values: int, n_escapes: int) -> int:
     (the formula of sf_expert_record_bytes)."""
     if n_values < 0 or not 0 <= n_escapes <= n_values:
         raise ValueError("invalid record counts")
-    return _align(n_values) + _align((n_values + 1) // 2) + _align(4 * n_escapes) + _align(n_escapes)
+    ec = section_offsets(n_values, n_escapes)[4]
+    return ec + _align(4 * (-(-n_values // CHUNK) + 1))
 
 
-def section_offsets(n_values: int, n_escapes: int) -> tuple[int, int, int, int]:
-    """Byte offsets of S, X, EI and EE in a record."""
+def section_offsets(n_values: int, n_escapes: int) -> tuple[int, int, int, int, int]:
+    """Byte offsets of S, X, EI, EE and EC in a record."""
     x = _align(n_values)
     ei = x + _align((n_values + 1) // 2)
     ee = ei + _align(4 * n_escapes)
-    return 0, x, ei, ee
+    ec = ee + _align(n_escapes)
+    return 0, x, ei, ee, ec
 
 
 @dataclass(frozen=True)
@@ -86,7 +89,7 @@ def encode_record(values: torch.Tensor, *, force: bool = False
     table = bytes(used.tolist()) + bytes(16 - used.numel())
     if size >= 2 * n and not force:
         return None, n_esc, table
-    _, off_x, off_ei, off_ee = section_offsets(n, n_esc)
+    _, off_x, off_ei, off_ee, off_ec = section_offsets(n, n_esc)
     rec = torch.zeros(size, dtype=torch.uint8, device=dev)
     rec[:n] = (((u >> 8) & 0x80) | (u & 0x7F)).to(torch.uint8)
     if n % 2:
@@ -95,6 +98,9 @@ def encode_record(values: torch.Tensor, *, force: bool = False
     if n_esc:
         rec[off_ei:off_ei + 4 * n_esc] = escapes.to(torch.int32).view(torch.uint8)
         rec[off_ee:off_ee + n_esc] = exponent[escapes].to(torch.uint8)
+    starts = torch.arange(0, n + CHUNK, CHUNK, device=dev)[:-(-n // CHUNK) + 1]
+    first = torch.searchsorted(escapes, starts).to(torch.int32)
+    rec[off_ec:off_ec + 4 * first.numel()] = first.view(torch.uint8)
     return rec, n_esc, table
 
 
@@ -168,7 +174,7 @@ def decode_record_reference(record, n_values: int, n_escapes: int, table: bytes)
     import numpy as np
 
     rec = np.asarray(record, dtype=np.uint8)
-    _, off_x, off_ei, off_ee = section_offsets(n_values, n_escapes)
+    _, off_x, off_ei, off_ee, _ = section_offsets(n_values, n_escapes)
     sm = rec[:n_values].astype(np.uint16)
     packed = rec[off_x:off_x + (n_values + 1) // 2]
     codes = np.empty(2 * packed.size, dtype=np.uint8)

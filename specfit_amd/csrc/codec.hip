@@ -8,7 +8,9 @@
 //   plane X: one 4-bit code per value (value 2j in the low nibble of byte j):
 //            code c < 15 stands for exponent table[c], code 15 for an escape;
 //   escapes: the index (uint32, ascending) and exponent byte of every value
-//            whose exponent is not in the table.
+//            whose exponent is not in the table, and for every chunk of
+//            SF_DECODE_CHUNK values the position of its first escape in that
+//            list (so a workgroup finds its escapes with two loads).
 // 12 bits per value plus the escapes: 75% of the raw bytes for experts whose
 // values fit 15 exponents.  The decode restores every value's 16 bits
 // exactly (no rounding anywhere), so a decoded slot holds the same bytes as
@@ -17,7 +19,8 @@
 // Record layout (byte offsets, every section 256-byte aligned):
 //   S at 0 (n bytes), X at align(n), escape indices at
 //   align(n) + align(ceil(n / 2)), escape exponents after them at
-//   + align(4 * escapes).
+//   + align(4 * escapes), the chunk table (ceil(n / SF_DECODE_CHUNK) + 1
+//   uint32) after those at + align(escapes).
 #include "sf_common.h"
 
 namespace {
@@ -25,6 +28,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kPerThread = 16;                           // values per thread
 constexpr int64_t kChunk = int64_t{kThreads} * kPerThread;  // values per workgroup
+static_assert(kChunk == SF_DECODE_CHUNK, "a workgroup decodes one chunk of the record");
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t{255}; }
 
@@ -33,6 +37,7 @@ struct DecodeArgs {
   const uint8_t* codes;     // plane X
   const uint32_t* esc_idx;  // escape indices, ascending
   const uint8_t* esc_exp;   // escape exponents
+  const uint32_t* chunk_esc;  // first escape of each chunk, [chunks + 1]
   uint16_t* out;            // bf16 [n]
   int64_t n;
   int n_esc;
@@ -45,22 +50,10 @@ __device__ __forceinline__ uint32_t join(uint32_t sm, uint32_t exponent) {
 
 __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
   __shared__ uint8_t table[16];
-  __shared__ int span[2];
   if (threadIdx.x < 16)
     table[threadIdx.x] = static_cast<uint8_t>(a.table[threadIdx.x >> 2] >> (8 * (threadIdx.x & 3)));
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
   const int64_t c1 = c0 + kChunk < a.n ? c0 + kChunk : a.n;
-  if (a.n_esc > 0 && threadIdx.x < 2) {
-    // First escape at or after c0 (thread 0) and after the chunk (thread 1).
-    const int64_t key = threadIdx.x == 0 ? c0 : c1;
-    int lo = 0, hi = a.n_esc;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (static_cast<int64_t>(a.esc_idx[mid]) < key) lo = mid + 1;
-      else hi = mid;
-    }
-    span[threadIdx.x] = lo;
-  }
   __syncthreads();
   const int64_t i = c0 + static_cast<int64_t>(threadIdx.x) * kPerThread;
   if (i + kPerThread <= a.n) {
@@ -88,8 +81,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     }
   }
   if (a.n_esc > 0) {
+    // The chunk's escapes, clamped to the list (a malformed table only
+    // skips or repeats patches inside the chunk, never writes outside it).
+    const int first = min(static_cast<int>(a.chunk_esc[blockIdx.x]), a.n_esc);
+    const int last = min(static_cast<int>(a.chunk_esc[blockIdx.x + 1]), a.n_esc);
     __syncthreads();  // the chunk's plain values are written
-    for (int e = span[0] + threadIdx.x; e < span[1]; e += kThreads) {
+    for (int e = first + static_cast<int>(threadIdx.x); e < last; e += kThreads) {
       const int64_t j = a.esc_idx[e];
       if (j >= c0 && j < c1) a.out[j] = static_cast<uint16_t>(join(a.sm[j], a.esc_exp[e]));
     }
@@ -98,12 +95,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+int64_t chunk_table_offset(int64_t n_values, int64_t n_escapes) {
+  return align256(n_values) + align256((n_values + 1) / 2) + align256(4 * n_escapes) +
+         align256(n_escapes);
+}
+
 }  // namespace
 
 extern "C" int64_t sf_expert_record_bytes(int64_t n_values, int64_t n_escapes) {
   if (n_values < 0 || n_escapes < 0 || n_escapes > n_values) return -1;
-  return align256(n_values) + align256((n_values + 1) / 2) + align256(4 * n_escapes) +
-         align256(n_escapes);
+  const int64_t chunks = (n_values + kChunk - 1) / kChunk;
+  return chunk_table_offset(n_values, n_escapes) + align256(4 * (chunks + 1));
 }
 
 extern "C" int sf_expert_decode(const void* record, size_t record_bytes, int64_t n_values,
@@ -122,6 +124,7 @@ extern "C" int sf_expert_decode(const void* record, size_t record_bytes, int64_t
   a.codes = base + align256(n_values);
   a.esc_idx = reinterpret_cast<const uint32_t*>(a.codes + align256((n_values + 1) / 2));
   a.esc_exp = reinterpret_cast<const uint8_t*>(a.esc_idx) + align256(4 * int64_t{n_escapes});
+  a.chunk_esc = reinterpret_cast<const uint32_t*>(base + chunk_table_offset(n_values, n_escapes));
   a.out = static_cast<uint16_t*>(out);
   a.n = n_values;
   a.n_esc = n_escapes;

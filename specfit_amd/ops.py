@@ -591,6 +591,27 @@ def copy_h2d(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) ->
     _native.check(rc, "sf_copy_h2d")
 
 
+def stage_record(staging_ptr: int, record_ptr: int, nbytes: int,
+                 stream: torch.cuda.Stream) -> None:
+    """sf_copy_h2d of a coded record (page-locked host) into a device
+    staging buffer, from pointers the caller has validated once (the expert
+    cache's per-transfer path; ``copy_h2d`` and ``expert_decode`` are the
+    checked forms)."""
+    if _recorder is not None:
+        _recorder._copy_started(stream, nbytes)
+    rc = _native.lib().sf_copy_h2d(staging_ptr, record_ptr, nbytes, int(stream.cuda_stream))
+    _native.check(rc, "sf_copy_h2d")
+
+
+def decode_staged(staging_ptr: int, nbytes: int, n_values: int, table_c, n_escapes: int,
+                  out_ptr: int, stream: torch.cuda.Stream) -> None:
+    """sf_expert_decode of a staged record into a slot, from validated
+    pointers and a ctypes uint8[16] exponent table."""
+    rc = _native.lib().sf_expert_decode(staging_ptr, nbytes, n_values, table_c, n_escapes,
+                                        out_ptr, int(stream.cuda_stream))
+    _native.check(rc, "sf_expert_decode")
+
+
 def expert_decode(record: torch.Tensor, n_escapes: int, table: bytes, out: torch.Tensor,
                   stream: torch.cuda.Stream | None = None) -> None:
     """out (bf16, on the device) <- the values of an exponent-coded expert

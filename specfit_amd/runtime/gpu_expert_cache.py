@@ -38,6 +38,7 @@ How this build holds that state:
 """
 from __future__ import annotations
 
+import ctypes
 import itertools
 from collections import deque
 from dataclasses import dataclass, field
@@ -64,6 +65,11 @@ _CLOSED = _lease_mod._CLOSED
 _READER_SPIN_NS = 200_000
 
 _versions = itertools.count(1)
+
+# Staging buffers of a cache with coded transfers: a buffer is reused four
+# transfers later, by when its decode has long run unless it waits for a
+# reader of its slot.
+_STAGING_BUFFERS = 4
 
 
 class _ResidentMap(dict):
@@ -201,10 +207,13 @@ class _RunPin:
             self._cache._unpin_many((self,))
 
 
-def _stage_sources(cpu_sources: Mapping, adopt: bool, owned: bool) -> tuple[dict, dict]:
+def _stage_sources(cpu_sources: Mapping, adopt: bool, owned: bool,
+                   coded: frozenset = frozenset()) -> tuple[dict, dict]:
     """(key -> page-locked tensor, key -> source order).  Adopted sources
     are used as they are; the others are copied into the rows of one
-    page-locked block allocated here."""
+    page-locked block allocated here.  Experts in ``coded`` always move as
+    coded records from their own page-locked blob, so their sources stay
+    as they are, page-locked or not."""
     items = tuple(cpu_sources.items())
     shape, dtype = items[0][1].shape, items[0][1].dtype
     to_pin = []
@@ -215,7 +224,7 @@ def _stage_sources(cpu_sources: Mapping, adopt: bool, owned: bool) -> tuple[dict
             raise ValueError("all expert sources must have the same shape")
         if src.dtype != dtype:
             raise ValueError("all expert sources must have the same dtype")
-        if not (adopt and src.is_pinned() and src.is_contiguous()):
+        if not (adopt and src.is_pinned() and src.is_contiguous()) and key not in coded:
             if owned:
                 raise ValueError("owned expert sources must be contiguous pinned CPU tensors")
             to_pin.append(key)
@@ -246,9 +255,10 @@ class GpuExpertCache:
         model share a pair (layers copy one after another; per-cache pairs
         of 48 layers ran at ~89% of the link rate one shared pair reaches).
         ``compressed_sources``: exponent-coded records of (some of) the
-        experts (specfit_amd.codec); their transfers move the record into
-        a device staging buffer and decode it into the slot, which then
-        holds the same bytes as a raw copy of the source."""
+        experts (specfit_amd.codec); their transfers copy the record into a
+        device staging buffer and decode it into the slot on the same copy
+        stream, and the slot then holds the same bytes as a raw copy of the
+        source."""
         if not cpu_sources:
             raise ValueError("cpu_sources must contain at least one expert")
         if slot_count <= 0:
@@ -269,15 +279,19 @@ class GpuExpertCache:
                        for s in copy_streams)):
             raise ValueError("copy_streams must be two distinct streams of the cache device")
 
-        self._sources, self._source_order = _stage_sources(
-            cpu_sources, adopt_pinned_sources, source_owner is not None)
+        coded = frozenset()
         if compressed_sources is not None:
             if not isinstance(compressed_sources, CompressedExperts):
                 raise ValueError("compressed_sources must be a CompressedExperts image")
-            if compressed_sources.numel != next(iter(self._sources.values())).numel():
+            if compressed_sources.numel != next(iter(cpu_sources.values())).numel():
                 raise ValueError("compressed_sources do not match the experts' size")
-            if any(key not in self._sources for key in compressed_sources.records):
+            if any(key not in cpu_sources for key in compressed_sources.records):
                 raise ValueError("compressed_sources hold an expert the cache does not know")
+            if compressed_sources.staging_bytes() and not compressed_sources.blob.is_pinned():
+                raise ValueError("compressed_sources must be in page-locked memory")
+            coded = frozenset(k for k, r in compressed_sources.records.items() if not r.raw)
+        self._sources, self._source_order = _stage_sources(
+            cpu_sources, adopt_pinned_sources, source_owner is not None, coded)
         # Each source key maps to itself: slots and maps hold these objects,
         # so lookups with them match by identity.
         self._key_objects = {key: key for key in self._sources}
@@ -291,10 +305,11 @@ class GpuExpertCache:
             self._own_copy_stream = self.copy_stream
             self._storage = torch.empty((slot_count, *first.shape), dtype=first.dtype,
                                         device=self.device)
-            # Two staging buffers for coded transfers (by submission parity).
+            # A ring of staging buffers for coded transfers (by submission
+            # sequence).
             staging = compressed_sources.staging_bytes() if compressed_sources else 0
             self._staging = [torch.empty(staging, dtype=torch.uint8, device=self.device)
-                             for _ in range(2 if staging else 0)]
+                             for _ in range(_STAGING_BUFFERS if staging else 0)]
             # The allocation may be recycled memory that kernels queued on the
             # current stream still read: order the first copies after them.
             here = torch.cuda.current_stream(self.device)
@@ -322,16 +337,31 @@ class GpuExpertCache:
         # (keys, resident-map version, table) of the last _slot_table.
         self._table_memo: tuple | None = None
         self._codec = compressed_sources
-        # (event, stream) after the decode that last read each staging buffer
-        self._staging_reader: list = [None, None]
+        # the (event, stream) after the decode that last read each staging buffer
+        self._staging_reader: list = [None] * len(self._staging)
+        # Per coded expert: (record pointer, bytes, escapes, ctypes exponent
+        # table), checked here once instead of on every transfer.
+        self._coded_args: dict = {}
+        if compressed_sources is not None:
+            blob = compressed_sources.blob.data_ptr()
+            for key, r in compressed_sources.records.items():
+                if not r.raw:
+                    self._coded_args[key] = (blob + r.offset, r.nbytes, r.n_escapes,
+                                             (ctypes.c_uint8 * 16).from_buffer_copy(r.table))
+        self._staging_ptrs = [b.data_ptr() for b in self._staging]
         self.h2d_bytes = 0  # bytes moved over the host link
 
     # ------------------------------------------------------------- queries --
     @property
     def sources_are_pinned(self) -> bool:
+        """Every host buffer a transfer copies from is page-locked (raw
+        sources, and the record blob of coded experts)."""
         if self._closed or self._closing:
             return False
-        return all(s.is_pinned() for s in self._sources.values())
+        codec = self._codec
+        records = codec.records if codec is not None else {}
+        return all(s.is_pinned() for k, s in self._sources.items()
+                   if k not in records or records[k].raw)
 
     @property
     def closed(self) -> bool:
@@ -796,7 +826,9 @@ class GpuExpertCache:
             self._key_objects.clear()
             self._codec = None
             self._staging = []
-            self._staging_reader = [None, None]
+            self._staging_reader = []
+            self._staging_ptrs = []
+            self._coded_args = {}
             owner, self._source_owner = self._source_owner, None
             if owner is not None:
                 owner.close()
@@ -860,13 +892,20 @@ class GpuExpertCache:
         readers = tuple(slot.use_events.values())
         slot.use_events.clear()
         stream = self._transfer_stream()
-        if slot.ready_event is not None and slot.write_stream is not stream:
-            # Writes of one slot stay in submission order across the two
-            # streams (on one stream, stream order already keeps them).
-            stream.wait_event(slot.ready_event)
-        for guard in readers:
-            self._await_reader(stream, guard)
-        staged = self._copy_in(slot, key, stream)
+        record = self._coded_args.get(key)
+        staged = None
+        if record is None:
+            if slot.ready_event is not None and slot.write_stream is not stream:
+                # Writes of one slot stay in submission order across the two
+                # streams (on one stream, stream order already keeps them).
+                stream.wait_event(slot.ready_event)
+            for guard in readers:
+                self._await_reader(stream, guard)
+            ops.copy_h2d(slot.tensor, self._sources[key], stream)
+            self.h2d_bytes += slot.tensor.numel() * slot.tensor.element_size()
+        else:
+            staged = self._stage_record(record, stream)
+            self._decode_into(slot, record, staged, stream, readers)
         ready = torch.cuda.Event(blocking=False)
         ready.record(stream)
         if staged is not None:
@@ -887,25 +926,30 @@ class GpuExpertCache:
                                     submission_sequence=transfer.submission_sequence,
                                     ready_event=ready)
 
-    def _copy_in(self, slot: _Slot, key: Hashable, stream: torch.cuda.Stream) -> int | None:
-        """Enqueue the expert's H2D into the slot on ``stream``: the raw
-        bytes, or its record into a staging buffer plus the decode into the
-        slot.  Returns the staging buffer used (None: raw copy)."""
-        codec = self._codec
-        rec = codec.records.get(key) if codec is not None else None
-        if rec is None or rec.raw:
-            ops.copy_h2d(slot.tensor, self._sources[key], stream)
-            self.h2d_bytes += slot.tensor.numel() * slot.tensor.element_size()
-            return None
-        j = self._submission_sequence & 1
+    def _stage_record(self, record: tuple, stream: torch.cuda.Stream) -> int:
+        """Enqueue the copy of a coded record into the next staging buffer
+        on the copy stream; returns the buffer.  The copy touches no slot,
+        so it waits for nothing but the decode that last read the buffer
+        (already ordered when that decode ran on the same stream)."""
+        j = self._submission_sequence % len(self._staging)
         last = self._staging_reader[j]
-        if last is not None and last[1] is not stream:
-            stream.wait_event(last[0])  # the previous decode out of this buffer
-        buf = self._staging[j][:rec.nbytes]
-        ops.copy_h2d(buf, codec.blob[rec.offset:rec.offset + rec.nbytes], stream)
-        ops.expert_decode(buf, rec.n_escapes, rec.table, slot.tensor, stream)
-        self.h2d_bytes += rec.nbytes
+        if last is not None and last[1] is not stream and not last[0].query():
+            stream.wait_event(last[0])
+        ops.stage_record(self._staging_ptrs[j], record[0], record[1], stream)
+        self.h2d_bytes += record[1]
         return j
+
+    def _decode_into(self, slot: _Slot, record: tuple, j: int, stream: torch.cuda.Stream,
+                     readers: tuple) -> None:
+        """Enqueue the decode of staging buffer j into the slot on the copy
+        stream, after the record's copy (stream order), the slot's previous
+        write and every stream that read the slot."""
+        if slot.ready_event is not None and slot.write_stream is not stream:
+            stream.wait_event(slot.ready_event)
+        for guard in readers:
+            self._await_reader(stream, guard)
+        ops.decode_staged(self._staging_ptrs[j], record[1], slot.tensor.numel(), record[3],
+                          record[2], slot.tensor.data_ptr(), stream)
 
     @staticmethod
     def _await_reader(stream: torch.cuda.Stream, guard: torch.cuda.Event) -> None:

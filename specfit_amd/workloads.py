@@ -74,18 +74,19 @@ def make_layer(*, seed: int = 0, hidden_size: int = 2048, num_experts: int = 128
 
 def make_layer_sources(layers: int, *, device, seed: int = 0, hidden_size: int = 2048,
                        num_experts: int = 128, intermediate_size: int = 768,
-                       std: float = 0.02) -> list[torch.Tensor]:
-    """Distinct packed experts for each of ``layers`` MoE layers, in page-locked
-    host memory: bf16 [E, 3*I*H] N(0, std) per layer (1.125 GiB at the
-    Qwen3-30B-A3B shape), drawn on ``device`` from a generator seeded with
-    seed + layer and copied to the host one expert block at a time."""
+                       std: float = 0.02, pin_memory: bool = True) -> list[torch.Tensor]:
+    """Distinct packed experts for each of ``layers`` MoE layers in host
+    memory (page-locked unless ``pin_memory`` is False): bf16 [E, 3*I*H]
+    N(0, std) per layer (1.125 GiB at the Qwen3-30B-A3B shape), drawn on
+    ``device`` from a generator seeded with seed + layer and copied to the
+    host one expert block at a time."""
     device = torch.device(device)
     E, row = num_experts, 3 * intermediate_size * hidden_size
     chunk = 16  # experts per device draw: 302 MB of fp32 at the 30B shape
     out = []
     for layer in range(layers):
         gen = torch.Generator(device=device).manual_seed(seed + layer)
-        host = torch.empty((E, row), dtype=torch.bfloat16, pin_memory=True)
+        host = torch.empty((E, row), dtype=torch.bfloat16, pin_memory=pin_memory)
         for e0 in range(0, E, chunk):
             n = min(chunk, E - e0)
             block = torch.empty((n, row), dtype=torch.float32, device=device)
@@ -124,7 +125,8 @@ QWEN3_30B_A3B_MODEL = dict(vocab_size=151936, hidden_size=2048, intermediate_siz
 def make_verify_model(*, device, layers: int = 48, slots_per_layer: int = 12, seed: int = 0,
                       experts: MoELayerWeights | None = None, std: float = 0.02,
                       expert_execution_policy: str = "resident_first",
-                      layer_sources: list[torch.Tensor] | None = None):
+                      layer_sources: list[torch.Tensor] | None = None,
+                      compress_expert_sources: bool = False):
     """A Qwen3-30B-A3B-shaped target for the verification forward, random
     init: every non-expert weight N(0, std) bf16 (norm weights 1), drawn on
     the device from a seeded generator.  The routed experts of layer l are
@@ -168,6 +170,7 @@ def make_verify_model(*, device, layers: int = 48, slots_per_layer: int = 12, se
         sources = {l: experts.experts for l in range(layers)}
     return build_offloaded_qwen3(model, device=device, slots_per_layer=slots_per_layer,
                                  layer_experts=sources,
+                                 compress_expert_sources=compress_expert_sources,
                                  expert_execution_policy=expert_execution_policy)
 
 

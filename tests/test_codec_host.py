@@ -16,11 +16,22 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.view(torch.int16).numpy().view(np.uint16)
 
 
+def _chunk_table_ok(rec: np.ndarray, n: int, n_esc: int) -> bool:
+    """EC[k] = number of escapes below value 4096 k, for k = 0 .. ceil(n/4096)."""
+    _, _, off_ei, _, off_ec = section_offsets(n, n_esc)
+    idx = rec[off_ei:off_ei + 4 * n_esc].view("<u4")
+    chunks = -(-n // 4096)
+    ec = rec[off_ec:off_ec + 4 * (chunks + 1)].view("<u4")
+    want = [int(np.count_nonzero(idx < 4096 * k)) for k in range(chunks + 1)]
+    return ec.tolist() == want
+
+
 def _roundtrip(values: torch.Tensor, force: bool = False):
     rec, n_esc, table = encode_record(values, force=force)
     assert rec is not None
     out = decode_record_reference(rec.numpy(), values.numel(), n_esc, table)
     assert np.array_equal(out, _bits(values))
+    assert _chunk_table_ok(rec.numpy(), values.numel(), n_esc)
     return rec, n_esc, table
 
 
@@ -29,7 +40,7 @@ def _roundtrip(values: torch.Tensor, force: bool = False):
 def test_record_size_matches_the_library(n, e):
     assert record_bytes(n, e) == _native.lib().sf_expert_record_bytes(n, e)
     off = section_offsets(n, e)
-    assert all(o % 256 == 0 for o in off) and off == tuple(sorted(off))
+    assert len(off) == 5 and all(o % 256 == 0 for o in off) and off == tuple(sorted(off))
     assert _native.lib().sf_expert_record_bytes(5, 6) == -1
     with pytest.raises(ValueError):
         record_bytes(5, 6)
@@ -42,7 +53,8 @@ def test_known_answer_record():
     assert n_esc == 0
     assert table == bytes([127, 126, 128]) + bytes(13)  # by count, ties to the lower exponent
     r = rec.numpy()
-    assert r.size == 512 and r[:5].tolist() == [0x00, 0x80, 0x00, 0x40, 0x00]
+    # S at 0, X at 256, no escapes, the chunk table [0, 0] at 512
+    assert r.size == 768 and r[:5].tolist() == [0x00, 0x80, 0x00, 0x40, 0x00]
     assert r[256:259].tolist() == [0x20, 0x01, 0x00]  # codes 0,2 | 1,0 | 0
     assert not r[5:256].any() and not r[259:].any()
     # too small to gain anything: the expert stays raw

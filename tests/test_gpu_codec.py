@@ -140,3 +140,29 @@ def test_coded_cache_under_copy_stream_switches(device, zipf_sources):
         assert _same_bits(got, packed[e].to(device)), f"expert {e}"
     cache.copy_stream = own
     cache.close()
+
+
+def test_coded_decode_waits_for_the_slot_reader(device, zipf_sources):
+    """One slot: a reader on another stream is still copying the slot out
+    (behind a bounded sleep kernel) when a miss evicts it.  The copy of the
+    new record may run at once; its decode must wait for the reader, which
+    then sees the old expert's bytes, and the slot ends with the new ones."""
+    packed, _, image = zipf_sources
+    cache = GpuExpertCache({ExpertKey(0, e): packed[e] for e in range(E)}, slot_count=1,
+                           device=device, adopt_pinned_sources=True, compressed_sources=image)
+    with cache.acquire(ExpertKey(0, 7)) as lease:
+        lease.wait()
+    torch.cuda.synchronize()
+    reader = torch.cuda.Stream(device=device)
+    with torch.cuda.stream(reader):
+        with cache.acquire(ExpertKey(0, 7)) as lease:
+            slot = lease.wait(reader)
+            torch.cuda._sleep(20_000_000)
+            seen = slot.clone()
+    with cache.acquire(ExpertKey(0, 8)) as lease:
+        new = lease.wait().clone()
+    torch.cuda.synchronize()
+    assert _same_bits(seen, packed[7].to(device))
+    assert _same_bits(new, packed[8].to(device))
+    assert cache.stats().h2d_submissions == 2 and cache.stats().evictions == 1
+    cache.close()

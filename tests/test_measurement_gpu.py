@@ -36,6 +36,10 @@ def test_bench_prints_one_contract_line(device):
     assert c["kind"] == "port" and c["value"] > 0 and c["cores"] >= 1 and c["sample"]
     assert d["device_ms_per_step"]["n"] == 2
     assert d["h2d"]["link_peak_gbs"] > 0 and 0 <= d["overlap"] <= 1
+    # coded transfers by default: ~75% of the expert bytes over the link
+    h = d["h2d"]
+    assert d["config"]["transfer"] == h["transfer"] == "coded"
+    assert 0.74 * h["expert_bytes"] < h["bytes"] < 0.76 * h["expert_bytes"]
 
 
 
@@ -55,7 +59,8 @@ def test_bench_48_layer_forward_under_the_prefetch_scheduler(device, workload, e
     assert len(lines) == 1, out.stdout[-2000:]
     d = json.loads(lines[0])
     assert d["value"] > 0 and d["config"]["executor"] == executor and d["config"]["layers"] == 2
-    assert "2 distinct pinned expert sets" in d["data"]
+    assert "2 distinct expert sets" in d["data"]
+    assert d["config"]["transfer"] == d["h2d"]["transfer"] == "coded"
     s = d["scheduler"]
     assert s["complete"] and 1 <= s["peak_inflight"] <= s["max_inflight"] == 2
     per = s["per_forward"]
