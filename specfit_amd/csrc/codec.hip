@@ -10,7 +10,8 @@
 //   escapes: the index (uint32, ascending) and exponent byte of every value
 //            whose exponent is not in the table, and for every chunk of
 //            SF_DECODE_CHUNK values the position of its first escape in that
-//            list (so a workgroup finds its escapes with two loads).
+//            list.  The decode reads only the exponents: an escape's position
+//            in the list is the chunk's first plus its rank in the chunk.
 // 12 bits per value plus the escapes: 75% of the raw bytes for experts whose
 // values fit 15 exponents.  The decode restores every value's 16 bits
 // exactly (no rounding anywhere), so a decoded slot holds the same bytes as
@@ -48,48 +49,100 @@ __device__ __forceinline__ uint32_t join(uint32_t sm, uint32_t exponent) {
   return ((sm & 0x80u) << 8) | (exponent << 7) | (sm & 0x7fu);
 }
 
+// Exclusive prefix over the wavefront of v (0 <= v <= 16) and the wavefront
+// total, from one ballot per bit of v.
+__device__ __forceinline__ int wave_prefix(int v, int& total) {
+  int prefix = 0;
+  total = 0;
+#pragma unroll
+  for (int b = 0; b < 5; ++b) {
+    const uint64_t m = __ballot((v >> b) & 1);
+    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+    prefix += below << b;
+    total += __popcll(m) << b;
+  }
+  return prefix;
+}
+
+// One workgroup per chunk; thread t decodes values c0 + 16 t .. + 15.  An
+// escaped value (code 15) takes the exponent at its rank among the chunk's
+// escapes (value order), counted from the chunk's first escape; the ranks
+// come from a workgroup prefix over per-thread escape counts, so every value
+// is written once and only escapes read the escape list.
 __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
   __shared__ uint8_t table[16];
-  if (threadIdx.x < 16)
-    table[threadIdx.x] = static_cast<uint8_t>(a.table[threadIdx.x >> 2] >> (8 * (threadIdx.x & 3)));
+  __shared__ int wave_total[kThreads / SF_WAVE];
+  const int tid = threadIdx.x;
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
-  const int64_t c1 = c0 + kChunk < a.n ? c0 + kChunk : a.n;
-  __syncthreads();
-  const int64_t i = c0 + static_cast<int64_t>(threadIdx.x) * kPerThread;
-  if (i + kPerThread <= a.n) {
+  const int64_t i = c0 + static_cast<int64_t>(tid) * kPerThread;
+  const int nv = i >= a.n ? 0 : (a.n - i < kPerThread ? static_cast<int>(a.n - i) : kPerThread);
+  uint32_t sw[4] = {0, 0, 0, 0};
+  uint32_t xw[2] = {0, 0};
+  if (nv == kPerThread) {
     const uint4 s = *reinterpret_cast<const uint4*>(a.sm + i);
     const uint2 x = *reinterpret_cast<const uint2*>(a.codes + (i >> 1));
-    const uint32_t sw[4] = {s.x, s.y, s.z, s.w};
-    const uint32_t xw[2] = {x.x, x.y};
-    uint32_t w[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      // values 2k and 2k+1 of the thread: bytes 2k, 2k+1 of S, byte k of X
-      const uint32_t sm0 = (sw[k >> 1] >> (16 * (k & 1))) & 0xffu;
-      const uint32_t sm1 = (sw[k >> 1] >> (16 * (k & 1) + 8)) & 0xffu;
-      const uint32_t xb = (xw[k >> 2] >> (8 * (k & 3))) & 0xffu;
-      w[k] = join(sm0, table[xb & 15u]) | (join(sm1, table[xb >> 4]) << 16);
-    }
-    uint4* o = reinterpret_cast<uint4*>(a.out + i);
-    o[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    o[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    sw[0] = s.x; sw[1] = s.y; sw[2] = s.z; sw[3] = s.w;
+    xw[0] = x.x; xw[1] = x.y;
   } else {
-    for (int64_t j = i; j < a.n && j < i + kPerThread; ++j) {
-      const uint32_t xb = a.codes[j >> 1];
-      const uint32_t code = (j & 1) ? xb >> 4 : xb & 15u;
-      a.out[j] = static_cast<uint16_t>(join(a.sm[j], table[code]));
+    // Tail of the record: values past n keep code 0 (never an escape).
+    for (int k = 0; k < nv; ++k) {
+      sw[k >> 2] |= static_cast<uint32_t>(a.sm[i + k]) << (8 * (k & 3));
+      const uint32_t xb = a.codes[(i + k) >> 1];
+      const uint32_t code = ((i + k) & 1) ? xb >> 4 : xb & 15u;
+      xw[k >> 3] |= code << (4 * (k & 7));
     }
   }
+  // The chunk's escapes: list positions [first, last) (clamped to the list,
+  // so a malformed table cannot read past it).
+  int first = 0, last = 0;
   if (a.n_esc > 0) {
-    // The chunk's escapes, clamped to the list (a malformed table only
-    // skips or repeats patches inside the chunk, never writes outside it).
-    const int first = min(static_cast<int>(a.chunk_esc[blockIdx.x]), a.n_esc);
-    const int last = min(static_cast<int>(a.chunk_esc[blockIdx.x + 1]), a.n_esc);
-    __syncthreads();  // the chunk's plain values are written
-    for (int e = first + static_cast<int>(threadIdx.x); e < last; e += kThreads) {
-      const int64_t j = a.esc_idx[e];
-      if (j >= c0 && j < c1) a.out[j] = static_cast<uint16_t>(join(a.sm[j], a.esc_exp[e]));
+    first = min(static_cast<int>(a.chunk_esc[blockIdx.x]), a.n_esc);
+    last = min(static_cast<int>(a.chunk_esc[blockIdx.x + 1]), a.n_esc);
+  }
+  if (tid < 16)
+    table[tid] = static_cast<uint8_t>(a.table[tid >> 2] >> (8 * (tid & 3)));
+  // 4-bit codes of the thread's values, and which are escapes.
+  uint32_t esc_mask = 0;
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k)
+    if (((xw[k >> 3] >> (4 * (k & 7))) & 15u) == 15u) esc_mask |= 1u << k;
+  int rank = first;
+  if (last > first) {  // uniform: the chunk has escapes
+    int total;
+    rank += wave_prefix(__popc(esc_mask), total);
+    if ((tid & (SF_WAVE - 1)) == 0) wave_total[tid / SF_WAVE] = total;
+  }
+  __syncthreads();  // the table (and the wavefront totals)
+  if (last > first) {
+    for (int w = 0; w < tid / SF_WAVE; ++w) rank += wave_total[w];
+  }
+  uint32_t w16[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t sm0 = (sw[k >> 1] >> (16 * (k & 1))) & 0xffu;
+    const uint32_t sm1 = (sw[k >> 1] >> (16 * (k & 1) + 8)) & 0xffu;
+    const uint32_t xb = (xw[k >> 2] >> (8 * (k & 3))) & 0xffu;
+    w16[k] = join(sm0, table[xb & 15u]) | (join(sm1, table[xb >> 4]) << 16);
+  }
+  // Escapes of this thread, in value order (rare: a few per expert chunk).
+  for (uint32_t m = esc_mask; m; m &= m - 1) {
+    const int k = __builtin_ctz(m);
+    if (rank < last) {
+      const uint32_t sm = (sw[k >> 2] >> (8 * (k & 3))) & 0xffu;
+      const uint32_t v = join(sm, a.esc_exp[rank]);
+      const int h = 16 * (k & 1);
+      w16[k >> 1] = (w16[k >> 1] & ~(0xffffu << h)) | (v << h);
     }
+    ++rank;
+  }
+  if (nv == kPerThread) {
+    uint4* o = reinterpret_cast<uint4*>(a.out + i);
+    o[0] = make_uint4(w16[0], w16[1], w16[2], w16[3]);
+    o[1] = make_uint4(w16[4], w16[5], w16[6], w16[7]);
+  } else {
+    for (int k = 0; k < nv; ++k)
+      a.out[i + k] = static_cast<uint16_t>(w16[k >> 1] >> (16 * (k & 1)));
   }
 }
 
