@@ -160,6 +160,21 @@ def cpu_baseline(layer, hidden_list, seconds: float) -> dict | None:
             "cpu_model": _cpu_model()}
 
 
+def decode_stats(rec) -> dict | None:
+    """The coded-transfer decodes of a recorded pass: count, average
+    event-bracketed duration on the copy stream (from the end of the
+    record's copy to the end of the decode), and algorithmic bytes (record
+    read + bf16 values written) over that time against the HBM peak."""
+    if not rec.decodes:
+        return None
+    t = sum(s.elapsed_time(e) for _, _, s, e in rec.decodes) * 1e-3
+    alg = sum(nbytes + 2 * n for nbytes, n, _, _ in rec.decodes)
+    n = len(rec.decodes)
+    return {"kernel": "decode_kernel (sf_expert_decode)", "count": n, "avg_us": t / n * 1e6,
+            "alg_bytes_per_decode": alg / n, "gbs": alg / t / 1e9,
+            "frac": alg / t / 1e9 / HBM_PEAK_GBS}
+
+
 def _union_length(spans) -> float:
     total, cur_s, cur_e = 0.0, None, None
     for s_, e_ in sorted(spans):
@@ -388,6 +403,7 @@ def main_verify(args) -> int:
         "cache": {"misses_per_layer": misses / (args.steps * args.layers),
                   "hits_per_layer": hits / (args.steps * args.layers)},
         "accepted_per_step": accepted / args.steps,
+        "decode": decode_stats(rec),
     }
     if sched_stats:  # the timed pass's forwards
         timed = sched_stats[args.warmup:args.warmup + args.steps]
@@ -508,6 +524,7 @@ def main_sweep(args) -> int:
             "h2d_expert_gbs": (rec_misses * layer.expert_bytes / h2d_time / 1e9
                                if h2d_time else None),
             "h2d_link_busy_frac": h2d_time / rec_wall if h2d_time else None,
+            "decode": decode_stats(rec),
         })
         log(f"T={T}: {points[-1]['tokens_per_s']:.0f} tokens/s, "
             f"{points[-1]['misses_per_step']:.2f} misses/step")
@@ -774,6 +791,7 @@ def main() -> int:
         "cache": {"misses_per_step": misses / args.steps, "hits_per_step": hits / args.steps},
         "overlap": overlap,
         "h2d_link_busy_frac": h2d_time / rec_wall if h2d_time else None,
+        "decode": decode_stats(rec),
         "k3_resident_in_step": {"launches": len(res), "gbs": res_bytes / res_time / 1e9 if res_time else None},
         "k3_all_resident": {"experts": len(active), "rows": rows_n, "us": res_launch * 1e6,
                             "gbs": res_launch_bytes / res_launch / 1e9,

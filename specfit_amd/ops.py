@@ -134,6 +134,9 @@ class LaunchRecorder:
         self.copies = copies
         self.h2d_bytes = 0
         self.h2d_count = 0
+        # (record bytes, values, start, end) of each coded-transfer decode,
+        # bracketed on its copy stream (start: after the record's copy).
+        self.decodes: list[tuple[int, int, TimingEvent, TimingEvent]] = []
         self.windows: list[tuple[TimingEvent, TimingEvent]] = []
         self._open: dict[int, tuple[torch.cuda.Stream, TimingEvent]] = {}
 
@@ -607,9 +610,16 @@ def decode_staged(staging_ptr: int, nbytes: int, n_values: int, table_c, n_escap
                   out_ptr: int, stream: torch.cuda.Stream) -> None:
     """sf_expert_decode of a staged record into a slot, from validated
     pointers and a ctypes uint8[16] exponent table."""
+    rec = _recorder
+    if rec is not None:
+        start, end = TimingEvent(), TimingEvent()
+        start.record(stream)
     rc = _native.lib().sf_expert_decode(staging_ptr, nbytes, n_values, table_c, n_escapes,
                                         out_ptr, int(stream.cuda_stream))
     _native.check(rc, "sf_expert_decode")
+    if rec is not None:
+        end.record(stream)
+        rec.decodes.append((nbytes, n_values, start, end))
 
 
 def expert_decode(record: torch.Tensor, n_escapes: int, table: bytes, out: torch.Tensor,

@@ -40,6 +40,8 @@ def test_bench_prints_one_contract_line(device):
     h = d["h2d"]
     assert d["config"]["transfer"] == h["transfer"] == "coded"
     assert 0.74 * h["expert_bytes"] < h["bytes"] < 0.76 * h["expert_bytes"]
+    dec = d["decode"]
+    assert dec["count"] == h["transfers"] and 0 < dec["frac"] < 1
 
 
 

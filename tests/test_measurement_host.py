@@ -148,6 +148,21 @@ def test_bench_helpers():
     assert 1.0 <= ratio < 1.2 and source.startswith("profiles/k3_traffic")
 
 
+def test_decode_stats():
+    class _Rec:
+        decodes = []
+
+    assert bench.decode_stats(_Rec()) is None
+    rec = _Rec()
+    # two decodes of a 100-byte record of 40 values, 0.002 and 0.004 ms
+    rec.decodes = [(100, 40, _Ev(0.0), _Ev(0.002)), (100, 40, _Ev(1.0), _Ev(1.004))]
+    d = bench.decode_stats(rec)
+    assert d["count"] == 2 and d["alg_bytes_per_decode"] == 180
+    assert d["avg_us"] == pytest.approx(3.0)
+    assert d["gbs"] == pytest.approx(360 / 6e-6 / 1e9)
+    assert d["frac"] == pytest.approx(d["gbs"] / bench.HBM_PEAK_GBS)
+
+
 @pytest.mark.parametrize("argv,steps", [([], 50), (["--workload", "verify48"], 10),
                                         (["--workload", "cold48"], 10), (["--steps", "7"], 7)])
 def test_bench_step_defaults(monkeypatch, argv, steps):
