@@ -783,6 +783,9 @@ def main() -> int:
         "h2d": {"achieved_gbs": h2d_bytes / h2d_time / 1e9 if h2d_time else None,
                 "expert_gbs": h2d_expert_bytes / h2d_time / 1e9 if h2d_time else None,
                 "transfer": args.transfer,
+                "bytes_note": "bytes: moved over the host link (coded records, or raw experts); "
+                              "expert_bytes: the bf16 expert bytes those transfers delivered to "
+                              "HBM",
                 "link_peak_gbs": best, "transfers": rec_misses, "bytes": h2d_bytes,
                 "expert_bytes": h2d_expert_bytes,
                 "busy_ms": h2d_time * 1e3,

@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 10
+#define SF_ABI_VERSION 11
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -261,30 +261,34 @@ int sf_copy_h2d(void *device_dst, const void *host_src, size_t bytes,
 /*
  * Exponent-coded expert records: the host-to-device transfer of an expert
  * may move a lossless record of its bf16 weights instead of the raw bytes
- * (about 75% of them for weights that span at most 15 binary exponents),
- * decoded into the slot on the device.  Together with sf_copy_h2d of the
- * record into a staging buffer this replaces the same
- * slot.tensor.copy_(pinned_source) (gpu_expert_cache.py:556-561); the slot
- * ends with the same bytes.  Record of n bf16 values with e escapes (every
- * section 256-byte aligned):
- *   S  [n] uint8            sign << 7 | mantissa of value i
- *   X  [ceil(n/2)] uint8    4-bit code of value i in byte i/2 (even i: low
- *                           nibble); code c < 15: exponent exponent_table[c];
- *                           code 15: an escape
- *   EI [e] uint32           ascending indices of the escaped values
- *   EE [e] uint8            their exponent bytes
- *   EC [c + 1] uint32       EC[k] = number of escapes below value
- *                           k * SF_DECODE_CHUNK (c = ceil(n / SF_DECODE_CHUNK))
+ * (about 69% of them for N(0, 0.02) weights), decoded into the slot on the
+ * device.  Together with sf_copy_h2d of the record into a staging buffer
+ * this replaces the same slot.tensor.copy_(pinned_source)
+ * (gpu_expert_cache.py:556-561); the slot ends with the same bytes.  Record
+ * of n bf16 values, q of them with a secondary code and r of those with a
+ * raw exponent (every section 256-byte aligned):
+ *   S  [n] uint8              sign << 7 | mantissa of value i
+ *   P  3 planes of ceil(n/16) uint16 words: bit i%16 of word i/16 of plane p
+ *                             is bit p of value i's primary code; code
+ *                             c < 7: exponent table[c]; 7: secondary
+ *   Q  [ceil(q/2)] uint8      4-bit secondary codes of the values with
+ *                             primary code 7, in value order (entry 2j in
+ *                             the low nibble of byte j); code c < 15:
+ *                             exponent table[16 + c]; 15: raw
+ *   R  [r] uint8              exponent bytes of the values with secondary
+ *                             code 15, in value order
+ *   QC, RC [c + 1] uint32     Q and R entries of the values before value
+ *                             k * SF_DECODE_CHUNK (c = ceil(n / SF_DECODE_CHUNK))
  * sf_expert_record_bytes returns the record size (-1 for invalid counts).
  * sf_expert_decode writes out[i] = sign | exponent | mantissa of value i:
  *   record          device buffer of at least record_bytes >= the record size
- *   exponent_table  host array of 16 exponent bytes (entry 15 is unused)
+ *   exponent_table  host array of 32 exponent bytes (entries 7 and 31 unused)
  *   out             bf16 [n_values], 16-byte aligned like record
  */
-int64_t sf_expert_record_bytes(int64_t n_values, int64_t n_escapes);
+int64_t sf_expert_record_bytes(int64_t n_values, int64_t n_secondary, int64_t n_raw);
 int sf_expert_decode(const void *record, size_t record_bytes, int64_t n_values,
-                     const uint8_t *exponent_table, int n_escapes, void *out,
-                     sf_stream_t stream);
+                     const uint8_t *exponent_table, int n_secondary, int n_raw,
+                     void *out, sf_stream_t stream);
 
 /*
  * K5: grouped-query attention of the verification forward over the cached

@@ -1,8 +1,8 @@
 """Host checks of the exponent-coded expert records (specfit_amd.codec):
-record sizes against the C library, a hand-built known answer, round trips
-through the host definition of the decode, the table rule and the raw
-fallback.  The device decode is checked against the same bytes in
-tests/test_gpu_codec.py."""
+record sizes against the C library, hand-built known answers, round trips
+through the host definition of the decode, the chunk tables, the table
+rules and the raw fallback.  The device decode is checked against the same
+bytes in tests/test_gpu_codec.py."""
 import numpy as np
 import pytest
 import torch
@@ -16,68 +16,99 @@ def _bits(t: torch.Tensor) -> np.ndarray:
     return t.view(torch.int16).numpy().view(np.uint16)
 
 
-def _chunk_table_ok(rec: np.ndarray, n: int, n_esc: int) -> bool:
-    """EC[k] = number of escapes below value 4096 k, for k = 0 .. ceil(n/4096)."""
-    _, _, off_ei, _, off_ec = section_offsets(n, n_esc)
-    idx = rec[off_ei:off_ei + 4 * n_esc].view("<u4")
+def _from_bits(bits) -> torch.Tensor:
+    return torch.tensor(np.asarray(bits, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
+
+
+def _chunk_tables_ok(rec: np.ndarray, values: torch.Tensor, q: int, r: int, table: bytes) -> bool:
+    """QC[k] / RC[k] = secondary / raw entries of the values below 4096 k."""
+    n = values.numel()
+    off = section_offsets(n, q, r)
+    exps = (_bits(values) >> 7) & 0xFF
+    distinct = len(set(exps.tolist()))
+    primary = list(table[:min(7, distinct)])  # the entries in use (the rest are padding)
+    secondary = list(table[16:16 + min(15, max(0, distinct - 7))])
+    in_primary = np.isin(exps, primary)
+    sec_pos = np.nonzero(~in_primary)[0]
+    raw_pos = sec_pos[~np.isin(exps[sec_pos], secondary)]
     chunks = -(-n // 4096)
-    ec = rec[off_ec:off_ec + 4 * (chunks + 1)].view("<u4")
-    want = [int(np.count_nonzero(idx < 4096 * k)) for k in range(chunks + 1)]
-    return ec.tolist() == want
+    qc = rec[off["QC"]:off["QC"] + 4 * (chunks + 1)].view("<u4")
+    rc = rec[off["RC"]:off["RC"] + 4 * (chunks + 1)].view("<u4")
+    want_q = [int(np.count_nonzero(sec_pos < 4096 * k)) for k in range(chunks + 1)]
+    want_r = [int(np.count_nonzero(raw_pos < 4096 * k)) for k in range(chunks + 1)]
+    return (len(sec_pos), len(raw_pos)) == (q, r) and qc.tolist() == want_q and rc.tolist() == want_r
 
 
 def _roundtrip(values: torch.Tensor, force: bool = False):
-    rec, n_esc, table = encode_record(values, force=force)
+    rec, q, r, table = encode_record(values, force=force)
     assert rec is not None
-    out = decode_record_reference(rec.numpy(), values.numel(), n_esc, table)
+    out = decode_record_reference(rec.numpy(), values.numel(), q, r, table)
     assert np.array_equal(out, _bits(values))
-    assert _chunk_table_ok(rec.numpy(), values.numel(), n_esc)
-    return rec, n_esc, table
+    return rec, q, r, table
 
 
-@pytest.mark.parametrize("n,e", [(0, 0), (1, 0), (5, 0), (4096, 3), (4_718_592, 700),
-                                 (4_718_593, 4_718_593)])
-def test_record_size_matches_the_library(n, e):
-    assert record_bytes(n, e) == _native.lib().sf_expert_record_bytes(n, e)
-    off = section_offsets(n, e)
-    assert len(off) == 5 and all(o % 256 == 0 for o in off) and off == tuple(sorted(off))
-    assert _native.lib().sf_expert_record_bytes(5, 6) == -1
+@pytest.mark.parametrize("n,q,r", [(0, 0, 0), (1, 0, 0), (5, 0, 0), (4096, 3, 1),
+                                   (4_718_592, 96_000, 700), (4_718_593, 4_718_593, 4_718_593)])
+def test_record_size_matches_the_library(n, q, r):
+    lib = _native.lib()
+    assert record_bytes(n, q, r) == lib.sf_expert_record_bytes(n, q, r)
+    off = section_offsets(n, q, r)
+    order = [off[k] for k in ("S", "P", "Q", "R", "QC", "RC", "size")]
+    assert all(o % 256 == 0 for o in order) and order == sorted(order)
+    assert lib.sf_expert_record_bytes(5, 6, 0) == -1 and lib.sf_expert_record_bytes(5, 2, 3) == -1
     with pytest.raises(ValueError):
-        record_bytes(5, 6)
+        record_bytes(5, 2, 3)
 
 
 def test_known_answer_record():
     # 1.0, -2.0, 0.5, 1.5, 1.0: exponents 127, 128, 126, 127, 127
     values = torch.tensor([1.0, -2.0, 0.5, 1.5, 1.0], dtype=torch.bfloat16)
-    rec, n_esc, table = encode_record(values, force=True)
-    assert n_esc == 0
-    assert table == bytes([127, 126, 128]) + bytes(13)  # by count, ties to the lower exponent
-    r = rec.numpy()
-    # S at 0, X at 256, no escapes, the chunk table [0, 0] at 512
-    assert r.size == 768 and r[:5].tolist() == [0x00, 0x80, 0x00, 0x40, 0x00]
-    assert r[256:259].tolist() == [0x20, 0x01, 0x00]  # codes 0,2 | 1,0 | 0
-    assert not r[5:256].any() and not r[259:].any()
+    rec, q, r, table = encode_record(values, force=True)
+    assert (q, r) == (0, 0)
+    # primary by count, ties to the lower exponent; no secondary exponents
+    assert table == bytes([127, 126, 128]) + bytes(13) + bytes(16)
+    b = rec.numpy()
+    # S at 0; planes at 256, 512, 768 (codes 0, 2, 1, 0, 0); QC at 1024, RC at 1280
+    assert b.size == 1536 and b[:5].tolist() == [0x00, 0x80, 0x00, 0x40, 0x00]
+    assert b[256:258].tolist() == [0b100, 0] and b[512:514].tolist() == [0b10, 0]
+    assert not b[768:].any() and not b[5:256].any() and not b[258:512].any()
+    assert not b[514:768].any()
     # too small to gain anything: the expert stays raw
     assert encode_record(values)[0] is None
+
+
+def test_known_answer_secondary_and_raw_codes():
+    # 23 exponents 100 .. 122: the first 7 twice, the others once (30 values)
+    exps = [100 + j for j in range(7)] * 2 + [107 + j for j in range(16)]
+    bits = [(e << 7) | (j % 128) | (0x8000 if j % 3 == 0 else 0) for j, e in enumerate(exps)]
+    values = _from_bits(bits)
+    rec, q, r, table = _roundtrip(values, force=True)
+    assert table[:7] == bytes(range(100, 107)) and table[7] == 0
+    assert table[16:31] == bytes(range(107, 122)) and table[31] == 0
+    assert (q, r) == (16, 1)  # exponents 107..122 go secondary, 122 raw
+    assert _chunk_tables_ok(rec.numpy(), values, q, r, table)
 
 
 def test_gaussian_expert_roundtrip_and_size():
     g = torch.Generator().manual_seed(3)
     values = (torch.randn(100_003, generator=g) * 0.02).to(torch.bfloat16)
-    rec, n_esc, table = _roundtrip(values)
-    assert n_esc < 100  # |x| < 2^-18 is rare at this scale
-    assert rec.numel() < 0.77 * 2 * values.numel()
-    # the table is the 15 most frequent exponents
+    rec, q, r, table = _roundtrip(values)
+    assert 0.01 < q / values.numel() < 0.03 and r < 100
+    assert rec.numel() < 0.70 * 2 * values.numel()
+    assert _chunk_tables_ok(rec.numpy(), values, q, r, table)
     exps = (_bits(values) >> 7) & 0xFF
     counts = np.bincount(exps, minlength=256)
-    top = sorted(range(256), key=lambda x: (-counts[x], x))[:15]
-    assert list(table[:15]) == top
+    ranked = [e for e in sorted(range(256), key=lambda x: (-counts[x], x)) if counts[e]]
+    sec = ranked[7:22]
+    assert list(table[:7]) == ranked[:7] and list(table[16:16 + len(sec)]) == sec
+    assert not any(table[16 + len(sec):])  # unused secondary entries are 0
 
 
 def test_every_bit_pattern_roundtrips():
     values = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
-    rec, n_esc, table = _roundtrip(values, force=True)
-    assert n_esc == 65536 - 15 * 256  # 15 exponents in the table, 256 values each
+    rec, q, r, table = _roundtrip(values, force=True)
+    assert (q, r) == (65536 - 7 * 256, 65536 - 22 * 256)
+    assert _chunk_tables_ok(rec.numpy(), values, q, r, table)
     # without force the record would be larger than the raw bytes
     assert encode_record(values)[0] is None
 
@@ -86,7 +117,8 @@ def test_every_bit_pattern_roundtrips():
 def test_short_and_odd_lengths(n):
     g = torch.Generator().manual_seed(n)
     values = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
-    _roundtrip(values, force=True)
+    rec, q, r, table = _roundtrip(values, force=True)
+    assert _chunk_tables_ok(rec.numpy(), values, q, r, table)
 
 
 def test_image_layout_and_raw_fallback():
@@ -108,7 +140,8 @@ def test_image_layout_and_raw_fallback():
     assert image.staging_bytes() == max(r.nbytes for r in coded)
     for e in range(3):
         r = image.records[("l", e)]
-        out = decode_record_reference(image.record_view(("l", e)).numpy(), n, r.n_escapes, r.table)
+        out = decode_record_reference(image.record_view(("l", e)).numpy(), n, r.n_secondary,
+                                      r.n_raw, r.table)
         assert np.array_equal(out, _bits(sources[("l", e)]))
     with pytest.raises(ValueError, match="stored raw"):
         image.record_view(("l", 3))
