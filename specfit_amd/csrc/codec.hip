@@ -16,7 +16,7 @@
 //   QC, RC  per chunk of SF_DECODE_CHUNK values, the number of Q and R
 //       entries of the values before it (chunks + 1 uint32 each).
 // About 11.1 bits per value for N(0, 0.02) weights (98% of values in 7
-// binades, all but ~0.02% in 22): 69% of the raw bytes.  The decode restores
+// binades, all but a few values per expert in 22): 69% of the raw bytes.  The decode restores
 // every value's 16 bits exactly, so a decoded slot holds the same bytes as a
 // raw copy.
 //
