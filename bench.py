@@ -71,7 +71,7 @@ def parse_args():
     p.add_argument("--verify-slots", type=int, default=12)
     p.add_argument("--transfer", choices=("raw", "coded"), default="coded",
                    help="what a miss moves over the host link: the expert's exponent-coded "
-                        "record (specfit_amd.codec, ~69%% of the bytes, decoded into the slot "
+                        "record (specfit_amd.codec, ~67%% of the bytes, decoded into the slot "
                         "on the device; the slot holds the same bytes), or its raw bf16 bytes")
     p.add_argument("--expert-sets", type=int, default=24,
                    help="48-layer forwards: distinct pinned expert sets (1.125 GiB each); layer l "

@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 11
+#define SF_ABI_VERSION 12
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -261,33 +261,38 @@ int sf_copy_h2d(void *device_dst, const void *host_src, size_t bytes,
 /*
  * Exponent-coded expert records: the host-to-device transfer of an expert
  * may move a lossless record of its bf16 weights instead of the raw bytes
- * (about 69% of them for N(0, 0.02) weights), decoded into the slot on the
+ * (about 67% of them for N(0, 0.02) weights), decoded into the slot on the
  * device.  Together with sf_copy_h2d of the record into a staging buffer
  * this replaces the same slot.tensor.copy_(pinned_source)
- * (gpu_expert_cache.py:556-561); the slot ends with the same bytes.  Record
- * of n bf16 values, q of them with a secondary code and r of those with a
- * raw exponent (every section 256-byte aligned):
- *   S  [n] uint8              sign << 7 | mantissa of value i
- *   P  3 planes of ceil(n/16) uint16 words: bit i%16 of word i/16 of plane p
- *                             is bit p of value i's primary code; code
- *                             c < 7: exponent table[c]; 7: secondary
- *   Q  [ceil(q/2)] uint8      4-bit secondary codes of the values with
- *                             primary code 7, in value order (entry 2j in
- *                             the low nibble of byte j); code c < 15:
- *                             exponent table[16 + c]; 15: raw
- *   R  [r] uint8              exponent bytes of the values with secondary
- *                             code 15, in value order
- *   QC, RC [c + 1] uint32     Q and R entries of the values before value
- *                             k * SF_DECODE_CHUNK (c = ceil(n / SF_DECODE_CHUNK))
- * sf_expert_record_bytes returns the record size (-1 for invalid counts).
+ * (gpu_expert_cache.py:556-561); the slot ends with the same bytes.  The
+ * exponent of a value is a cascade of codes into the 32-byte table:
+ *   level 1, 2 bits (every value):       c < 3: table[c];       3: level 2
+ *   level 2, 2 bits (n2 values):         c < 3: table[8 + c];   3: level 3
+ *   level 3, 4 bits (n3 values):         c < 15: table[16 + c]; 15: raw byte
+ * Record of n values (every section 256-byte aligned):
+ *   S   [n] uint8                 sign << 7 | mantissa of value i
+ *   P   2 planes of ceil(n/16) uint16 words: bit i%16 of word i/16 of
+ *                                 plane p is bit p of value i's level-1 code
+ *   L2  [ceil(n2/4)] uint8        level-2 codes in value order, entry j at
+ *                                 bits 2(j%4) of byte j/4
+ *   L3  [ceil(n3/2)] uint8        level-3 codes in value order, entry j at
+ *                                 bits 4(j%2) of byte j/2
+ *   R   [nr] uint8                raw exponent bytes in value order
+ *   C2, C3, CR [c + 1] uint32     L2, L3 and R entries of the values before
+ *                                 value k * SF_DECODE_CHUNK
+ *                                 (c = ceil(n / SF_DECODE_CHUNK))
+ * sf_expert_record_bytes returns the record size (-1 for invalid counts;
+ * valid: 0 <= n_raw <= n_third <= n_second <= n_values).
  * sf_expert_decode writes out[i] = sign | exponent | mantissa of value i:
  *   record          device buffer of at least record_bytes >= the record size
- *   exponent_table  host array of 32 exponent bytes (entries 7 and 31 unused)
+ *   exponent_table  host array of 32 exponent bytes (entries 3..7, 11..15
+ *                   and 31 unused)
  *   out             bf16 [n_values], 16-byte aligned like record
  */
-int64_t sf_expert_record_bytes(int64_t n_values, int64_t n_secondary, int64_t n_raw);
+int64_t sf_expert_record_bytes(int64_t n_values, int64_t n_second, int64_t n_third,
+                               int64_t n_raw);
 int sf_expert_decode(const void *record, size_t record_bytes, int64_t n_values,
-                     const uint8_t *exponent_table, int n_secondary, int n_raw,
+                     const uint8_t *exponent_table, int n_second, int n_third, int n_raw,
                      void *out, sf_stream_t stream);
 
 /*

@@ -10,7 +10,7 @@ import threading
 
 from .build import LIB_PATH
 
-SF_ABI_VERSION = 11
+SF_ABI_VERSION = 12
 SF_ERR_HIP_BASE = 1000
 
 _lock = threading.Lock()
@@ -35,8 +35,8 @@ SIGNATURES = {
     "sf_expert_swiglu": ([_p, _i, _i64, _i, _i, _p, _p, _p, _p], _i),
     "sf_combine": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p], _i),
     "sf_copy_h2d": ([_p, _p, _sz, _p], _i),
-    "sf_expert_record_bytes": ([_i64, _i64, _i64], _i64),
-    "sf_expert_decode": ([_p, _sz, _i64, _p, _i, _i, _p, _p], _i),
+    "sf_expert_record_bytes": ([_i64, _i64, _i64, _i64], _i64),
+    "sf_expert_decode": ([_p, _sz, _i64, _p, _i, _i, _i, _p, _p], _i),
     "sf_tree_attention": ([_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64,
                            _i, _i, _i, _i, _i, ctypes.c_float, _p, _p], _i),
     "sf_rms_norm": ([_p, _i64, _i, _i, _p, ctypes.c_float, _p, _i64, _p], _i),

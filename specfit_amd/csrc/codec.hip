@@ -2,28 +2,34 @@
 //
 // An expert moves over the host link as an exponent-coded record of its bf16
 // weights instead of the raw 2 bytes per value.  A bf16 value is
-// sign (1 bit) | exponent (8 bits) | mantissa (7 bits), and the weights of
-// an expert concentrate their exponents in a few binades.  The record:
-//   S   one byte per value, sign << 7 | mantissa;
-//   P   a 3-bit primary code per value, as three bit planes (plane p holds
-//       bit p of the codes of values 16g .. 16g+15 in its uint16 word g):
-//       code c < 7 stands for exponent primary[c], code 7 for "secondary";
-//   Q   one 4-bit secondary code per value with primary code 7, in value
-//       order (entry 2j in the low nibble of byte j): code c < 15 stands for
-//       exponent secondary[c], code 15 for "raw";
-//   R   the exponent byte of every value with secondary code 15, in value
-//       order;
-//   QC, RC  per chunk of SF_DECODE_CHUNK values, the number of Q and R
-//       entries of the values before it (chunks + 1 uint32 each).
-// About 11.1 bits per value for N(0, 0.02) weights (98% of values in 7
-// binades, all but a few values per expert in 22): 69% of the raw bytes.  The decode restores
+// sign (1 bit) | exponent (8 bits) | mantissa (7 bits).  The sign and
+// mantissa bits of weights are close to uniform and stay as they are; the
+// exponents concentrate in a few binades and take a cascade of short codes,
+// each level a fixed-width code into a small table of the expert's own whose
+// last code defers to the next level:
+//   level 1  2 bits, every value:              c < 3: table[c],      3: level 2
+//   level 2  2 bits, values with level-1 3:    c < 3: table[8 + c],  3: level 3
+//   level 3  4 bits, values with level-2 3:    c < 15: table[16 + c], 15: raw
+//   raw      the exponent byte.
+// The record:
+//   S       one byte per value, sign << 7 | mantissa;
+//   P       the level-1 codes as two bit planes (plane p holds bit p of the
+//           codes of values 16g .. 16g+15 in its uint16 word g);
+//   L2, L3  the level-2 and level-3 codes in value order, packed from bit 0
+//           of byte 0 upwards (2 and 4 bits per entry);
+//   R       the raw exponent bytes in value order;
+//   C2, C3, CR  per chunk of SF_DECODE_CHUNK values, the L2, L3 and R
+//           entries of the values before it (chunks + 1 uint32 each).
+// About 10.7 bits per value for N(0, 0.02) weights (73% of values in 3
+// binades, all but 4% in 6): 67% of the raw bytes.  The decode restores
 // every value's 16 bits exactly, so a decoded slot holds the same bytes as a
 // raw copy.
 //
 // Record layout (byte offsets, every section 256-byte aligned), for n
-// values, q secondary and r raw entries:
-//   S at 0 [n], P at align(n) [3 planes of 2 * ceil(n / 16) bytes, each
-//   aligned], Q [ceil(q / 2)], R [r], QC [4 (chunks + 1)], RC [4 (chunks + 1)].
+// values with n2, n3 and nr entries in L2, L3 and R:
+//   S at 0 [n], P at align(n) [2 planes of 2 * ceil(n / 16) bytes, each
+//   aligned], L2 [ceil(n2 / 4)], L3 [ceil(n3 / 2)], R [nr],
+//   C2, C3, CR [4 (chunks + 1)] each.
 #include "sf_common.h"
 
 namespace {
@@ -37,35 +43,39 @@ constexpr int kWaves = kThreads / SF_WAVE;
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t{255}; }
 
 struct Layout {
-  int64_t plane, q, r, qc, rc, total;  // byte offsets of P plane 0, Q, R, QC, RC; size
+  int64_t plane, l2, l3, r, c2, c3, cr, total;  // byte offsets of the sections; size
 };
 
-Layout layout(int64_t n, int64_t q, int64_t r) {
+Layout layout(int64_t n, int64_t n2, int64_t n3, int64_t nr) {
   Layout l;
   const int64_t chunks = (n + kChunk - 1) / kChunk;
   const int64_t plane_bytes = align256(2 * ((n + 15) / 16));
+  const int64_t table_bytes = align256(4 * (chunks + 1));
   l.plane = align256(n);
-  l.q = l.plane + 3 * plane_bytes;
-  l.r = l.q + align256((q + 1) / 2);
-  l.qc = l.r + align256(r);
-  l.rc = l.qc + align256(4 * (chunks + 1));
-  l.total = l.rc + align256(4 * (chunks + 1));
+  l.l2 = l.plane + 2 * plane_bytes;
+  l.l3 = l.l2 + align256((n2 + 3) / 4);
+  l.r = l.l3 + align256((n3 + 1) / 2);
+  l.c2 = l.r + align256(nr);
+  l.c3 = l.c2 + table_bytes;
+  l.cr = l.c3 + table_bytes;
+  l.total = l.cr + table_bytes;
   return l;
 }
 
 struct DecodeArgs {
-  const uint8_t* sm;       // S
-  const uint16_t* planes;  // P plane 0; plane p at planes + p * plane_words
+  const uint8_t* sm;        // S
+  const uint16_t* planes;   // P plane 0; plane 1 at planes + plane_words
   int64_t plane_words;
-  const uint8_t* sec;      // Q
-  const uint8_t* raw;      // R
-  const uint32_t* q_chunk; // QC
-  const uint32_t* r_chunk; // RC
-  uint16_t* out;           // bf16 [n]
+  const uint32_t* l2;       // L2 as words (the section is 256-byte aligned)
+  const uint32_t* l3;       // L3 as words
+  const uint8_t* raw;       // R
+  const uint32_t* c2;       // C2, C3, CR
+  const uint32_t* c3;
+  const uint32_t* cr;
+  uint16_t* out;            // bf16 [n]
   int64_t n;
-  int n_sec;
-  int n_raw;
-  uint32_t table[8];       // bytes 0..7: primary exponents; 16..31: secondary
+  int n2, n3, nr;
+  uint32_t table[8];        // bytes 0..2: level 1; 8..10: level 2; 16..30: level 3
 };
 
 __device__ __forceinline__ uint32_t join(uint32_t sm, uint32_t exponent) {
@@ -92,28 +102,54 @@ __device__ __forceinline__ int workgroup_prefix(int v, int* wave_total) {
   return prefix;
 }
 
-// One workgroup per chunk; thread t decodes values c0 + 16 t .. + 15.  A
-// value with primary code 7 takes the secondary code at its rank among the
-// chunk's primary escapes (value order) from the chunk's first Q entry; one
-// with secondary code 15 takes the raw exponent at its rank among the
-// chunk's raw entries.  Ranks come from workgroup prefixes over per-thread
-// counts, so every value is written once.
+// Bits bit0 .. bit0 + nbits - 1 (nbits <= 64) of a packed list, bit j of
+// the result = list bit bit0 + j.  Loads only the words that hold those
+// bits, which lie inside the list's bytes.
+__device__ __forceinline__ uint64_t read_bits(const uint32_t* w, int64_t bit0, int nbits) {
+  if (nbits <= 0) return 0;
+  const int64_t first = bit0 >> 5;
+  const int64_t last = (bit0 + nbits - 1) >> 5;
+  const int sh = static_cast<int>(bit0 & 31);
+  uint64_t v = static_cast<uint64_t>(w[first]) >> sh;
+  if (last > first) v |= static_cast<uint64_t>(w[first + 1]) << (32 - sh);
+  if (last > first + 1) v |= static_cast<uint64_t>(w[first + 2]) << (64 - sh);  // sh > 0 here
+  return nbits == 64 ? v : v & ((uint64_t{1} << nbits) - 1);
+}
+
+// Clamped entry range [first, last) of one list for chunk `chunk`: a
+// malformed table can only skip or repeat entries, never read past a list.
+__device__ __forceinline__ void chunk_range(const uint32_t* table, int count, int chunk,
+                                            int& first, int& last) {
+  first = last = 0;
+  if (count > 0) {
+    first = min(static_cast<int>(table[chunk]), count);
+    last = min(static_cast<int>(table[chunk + 1]), count);
+  }
+}
+
+// One workgroup per chunk; thread t decodes values 16 t .. 16 t + 15 of
+// it.  A value that reaches level 2 or 3 takes the code at its rank among
+// the chunk's values that reach that level, counted from the chunk's first
+// entry of that level's list; a raw exponent likewise.  Ranks come from workgroup
+// prefixes over per-thread counts (skipped for a list the chunk has no
+// entries of), so every value is written once.  Entries a malformed record
+// lacks count as the next level's escape; a value left without a raw byte
+// keeps exponent 0.
 __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
   __shared__ uint8_t table[32];
-  __shared__ int wave_total[2][kWaves];
+  __shared__ int wave_total[3][kWaves];
   const int tid = threadIdx.x;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
-  const int64_t i = c0 + static_cast<int64_t>(tid) * kPerThread;
+  const int chunk = blockIdx.x;
+  const int64_t i = static_cast<int64_t>(chunk) * kChunk + static_cast<int64_t>(tid) * kPerThread;
   const int nv = i >= a.n ? 0 : (a.n - i < kPerThread ? static_cast<int>(a.n - i) : kPerThread);
   const int64_t g = i / kPerThread;  // the thread's word in each plane
   uint32_t sw[4] = {0, 0, 0, 0};
-  uint32_t p0 = 0, p1 = 0, p2 = 0;
+  uint32_t p0 = 0, p1 = 0;
   if (nv > 0) {
     // Plane words exist for every group, a partial last one included (its
     // bits past n are 0).
     p0 = a.planes[g];
     p1 = a.planes[a.plane_words + g];
-    p2 = a.planes[2 * a.plane_words + g];
   }
   if (nv == kPerThread) {
     const uint4 s = *reinterpret_cast<const uint4*>(a.sm + i);
@@ -121,64 +157,65 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
   } else {
     for (int k = 0; k < nv; ++k) sw[k >> 2] |= static_cast<uint32_t>(a.sm[i + k]) << (8 * (k & 3));
   }
-  // The chunk's Q and R ranges, clamped to the lists (a malformed table can
-  // only skip or repeat entries, never read past a list).
-  int q_first = 0, q_last = 0, r_first = 0, r_last = 0;
-  if (a.n_sec > 0) {
-    q_first = min(static_cast<int>(a.q_chunk[blockIdx.x]), a.n_sec);
-    q_last = min(static_cast<int>(a.q_chunk[blockIdx.x + 1]), a.n_sec);
-  }
-  if (a.n_raw > 0) {
-    r_first = min(static_cast<int>(a.r_chunk[blockIdx.x]), a.n_raw);
-    r_last = min(static_cast<int>(a.r_chunk[blockIdx.x + 1]), a.n_raw);
-  }
+  int f2, l2, f3, l3, fr, lr;
+  chunk_range(a.c2, a.n2, chunk, f2, l2);
+  chunk_range(a.c3, a.n3, chunk, f3, l3);
+  chunk_range(a.cr, a.nr, chunk, fr, lr);
   if (tid < 32) table[tid] = static_cast<uint8_t>(a.table[tid >> 2] >> (8 * (tid & 3)));
-  // Primary codes (bit j of p0 | p1 << 1 | p2 << 2); code 7 is an escape.
-  const uint32_t esc1 = p0 & p1 & p2;
-  int q_rank = q_first;
-  if (q_last > q_first) q_rank += workgroup_prefix(__popc(esc1), wave_total[0]);
-  __syncthreads();  // the tables
+
+  // Level 2: this thread's entries are consecutive in L2 from rank r2.
+  const uint32_t esc1 = p0 & p1;
+  const int k1 = __popc(esc1);
+  int r2 = f2;
+  if (l2 > f2) r2 += workgroup_prefix(k1, wave_total[0]);
+  const int v2 = max(0, min(k1, l2 - r2));
+  uint32_t codes2 = static_cast<uint32_t>(read_bits(a.l2, 2 * static_cast<int64_t>(r2), 2 * v2));
+  if (v2 < k1) codes2 |= ~0u << (2 * v2);  // missing entries escape
+  const uint32_t at3 = codes2 & (codes2 >> 1) & 0x55555555u;  // bit 2j: entry j is code 3
+  uint32_t esc2 = 0;
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int j = __popc(esc1 & ((1u << k) - 1));
+    esc2 |= ((esc1 >> k) & (at3 >> (2 * j)) & 1u) << k;
+  }
+
+  // Level 3: consecutive in L3 from rank r3.
+  const int k2 = __popc(esc2);
+  int r3 = f3;
+  if (l3 > f3) r3 += workgroup_prefix(k2, wave_total[1]);
+  const int v3 = max(0, min(k2, l3 - r3));
+  uint64_t codes3 = read_bits(a.l3, 4 * static_cast<int64_t>(r3), 4 * v3);
+  if (v3 < k2) codes3 |= ~uint64_t{0} << (4 * v3);
+  uint32_t esc3 = 0;
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int j = __popc(esc2 & ((1u << k) - 1));
+    const uint32_t c = static_cast<uint32_t>(codes3 >> (4 * j)) & 15u;
+    esc3 |= static_cast<uint32_t>((esc2 >> k) & 1u & (c == 15u)) << k;
+  }
+
+  // Raw exponents: consecutive in R from rank rr.
+  int rr = fr;
+  if (lr > fr) rr += workgroup_prefix(__popc(esc3), wave_total[2]);
+  __syncthreads();  // the table
+
   uint32_t w16[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    uint32_t v[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = 2 * k + h;
-      const uint32_t c = ((p0 >> j) & 1u) | (((p1 >> j) & 1u) << 1) | (((p2 >> j) & 1u) << 2);
-      v[h] = join((sw[j >> 2] >> (8 * (j & 3))) & 0xffu, table[c]);
-    }
-    w16[k] = v[0] | (v[1] << 16);
-  }
-  // Secondary codes of this thread's escapes, in value order, packed four
-  // bits per value; the raw ones among them are counted for their ranks.
-  uint64_t sec_codes = 0;
-  uint32_t raw_mask = 0;
-  for (uint32_t m = esc1; m; m &= m - 1) {
-    const int k = __builtin_ctz(m);
-    uint32_t c = 15;
-    if (q_rank < q_last) {
-      const uint32_t byte = a.sec[q_rank >> 1];
-      c = (q_rank & 1) ? byte >> 4 : byte & 15u;
-    }
-    sec_codes |= static_cast<uint64_t>(c) << (4 * k);
-    if (c == 15) raw_mask |= 1u << k;
-    ++q_rank;
-  }
-  int r_rank = r_first;
-  if (r_last > r_first) r_rank += workgroup_prefix(__popc(raw_mask), wave_total[1]);
-  for (uint32_t m = esc1; m; m &= m - 1) {
-    const int k = __builtin_ctz(m);
-    uint32_t e;
-    if (raw_mask & (1u << k)) {
-      if (r_rank >= r_last) continue;  // malformed record: leave the value
-      e = a.raw[r_rank++];
-    } else {
-      e = table[16 + ((sec_codes >> (4 * k)) & 15u)];
+  for (int k = 0; k < kPerThread; ++k) {
+    const uint32_t c1 = ((p0 >> k) & 1u) | (((p1 >> k) & 1u) << 1);
+    const int j2 = __popc(esc1 & ((1u << k) - 1));
+    const int j3 = __popc(esc2 & ((1u << k) - 1));
+    const uint32_t c2 = (codes2 >> (2 * j2)) & 3u;
+    const uint32_t c3 = static_cast<uint32_t>(codes3 >> (4 * j3)) & 15u;
+    const uint32_t idx = c1 != 3u ? c1 : (c2 != 3u ? 8u + c2 : 16u + c3);
+    uint32_t e = table[idx];
+    if ((esc3 >> k) & 1u) {
+      const int rank = rr + __popc(esc3 & ((1u << k) - 1));
+      e = rank < lr ? a.raw[rank] : 0u;
     }
     const uint32_t v = join((sw[k >> 2] >> (8 * (k & 3))) & 0xffu, e);
-    const int h = 16 * (k & 1);
-    w16[k >> 1] = (w16[k >> 1] & ~(0xffffu << h)) | (v << h);
+    if (k & 1) w16[k >> 1] |= v << 16;
+    else w16[k >> 1] = v;
   }
   if (nv == kPerThread) {
     uint4* o = reinterpret_cast<uint4*>(a.out + i);
@@ -191,26 +228,26 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-bool counts_valid(int64_t n, int64_t q, int64_t r) {
-  return n >= 0 && q >= 0 && r >= 0 && q <= n && r <= q;
+bool counts_valid(int64_t n, int64_t n2, int64_t n3, int64_t nr) {
+  return n >= 0 && nr >= 0 && nr <= n3 && n3 <= n2 && n2 <= n;
 }
 
 }  // namespace
 
-extern "C" int64_t sf_expert_record_bytes(int64_t n_values, int64_t n_secondary,
+extern "C" int64_t sf_expert_record_bytes(int64_t n_values, int64_t n_second, int64_t n_third,
                                           int64_t n_raw) {
-  if (!counts_valid(n_values, n_secondary, n_raw)) return -1;
-  return layout(n_values, n_secondary, n_raw).total;
+  if (!counts_valid(n_values, n_second, n_third, n_raw)) return -1;
+  return layout(n_values, n_second, n_third, n_raw).total;
 }
 
 extern "C" int sf_expert_decode(const void* record, size_t record_bytes, int64_t n_values,
-                                const uint8_t* exponent_table, int n_secondary, int n_raw,
-                                void* out, sf_stream_t stream) {
-  if (!counts_valid(n_values, n_secondary, n_raw) || n_values > 0xffffffffLL)
+                                const uint8_t* exponent_table, int n_second, int n_third,
+                                int n_raw, void* out, sf_stream_t stream) {
+  if (!counts_valid(n_values, n_second, n_third, n_raw) || n_values > 0xffffffffLL)
     return SF_ERR_INVALID_ARGUMENT;
   if (n_values == 0) return SF_OK;
   if (!record || !exponent_table || !out) return SF_ERR_INVALID_ARGUMENT;
-  const Layout l = layout(n_values, n_secondary, n_raw);
+  const Layout l = layout(n_values, n_second, n_third, n_raw);
   if (static_cast<int64_t>(record_bytes) < l.total) return SF_ERR_INVALID_ARGUMENT;
   if (!aligned16(record) || !aligned16(out)) return SF_ERR_MISALIGNED;
   const uint8_t* base = static_cast<const uint8_t*>(record);
@@ -218,14 +255,17 @@ extern "C" int sf_expert_decode(const void* record, size_t record_bytes, int64_t
   a.sm = base;
   a.planes = reinterpret_cast<const uint16_t*>(base + l.plane);
   a.plane_words = align256(2 * ((n_values + 15) / 16)) / 2;
-  a.sec = base + l.q;
+  a.l2 = reinterpret_cast<const uint32_t*>(base + l.l2);
+  a.l3 = reinterpret_cast<const uint32_t*>(base + l.l3);
   a.raw = base + l.r;
-  a.q_chunk = reinterpret_cast<const uint32_t*>(base + l.qc);
-  a.r_chunk = reinterpret_cast<const uint32_t*>(base + l.rc);
+  a.c2 = reinterpret_cast<const uint32_t*>(base + l.c2);
+  a.c3 = reinterpret_cast<const uint32_t*>(base + l.c3);
+  a.cr = reinterpret_cast<const uint32_t*>(base + l.cr);
   a.out = static_cast<uint16_t*>(out);
   a.n = n_values;
-  a.n_sec = n_secondary;
-  a.n_raw = n_raw;
+  a.n2 = n_second;
+  a.n3 = n_third;
+  a.nr = n_raw;
   for (int c = 0; c < 32; ++c)
     a.table[c >> 2] |= static_cast<uint32_t>(exponent_table[c]) << (8 * (c & 3));
   const int64_t blocks = (n_values + kChunk - 1) / kChunk;

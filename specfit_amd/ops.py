@@ -606,36 +606,40 @@ def stage_record(staging_ptr: int, record_ptr: int, nbytes: int,
     _native.check(rc, "sf_copy_h2d")
 
 
-def decode_staged(staging_ptr: int, nbytes: int, n_values: int, table_c, n_secondary: int,
-                  n_raw: int, out_ptr: int, stream: torch.cuda.Stream) -> None:
+def decode_staged(staging_ptr: int, nbytes: int, n_values: int, table_c, counts: tuple,
+                  out_ptr: int, stream: torch.cuda.Stream) -> None:
     """sf_expert_decode of a staged record into a slot, from validated
-    pointers and a ctypes uint8[32] exponent table."""
+    pointers, a ctypes uint8[32] exponent table and the record's
+    (n_second, n_third, n_raw)."""
     rec = _recorder
     if rec is not None:
         start, end = TimingEvent(), TimingEvent()
         start.record(stream)
-    rc = _native.lib().sf_expert_decode(staging_ptr, nbytes, n_values, table_c, n_secondary,
-                                        n_raw, out_ptr, int(stream.cuda_stream))
+    rc = _native.lib().sf_expert_decode(staging_ptr, nbytes, n_values, table_c, counts[0],
+                                        counts[1], counts[2], out_ptr, int(stream.cuda_stream))
     _native.check(rc, "sf_expert_decode")
     if rec is not None:
         end.record(stream)
         rec.decodes.append((nbytes, n_values, start, end))
 
 
-def expert_decode(record: torch.Tensor, n_secondary: int, n_raw: int, table: bytes,
-                  out: torch.Tensor, stream: torch.cuda.Stream | None = None) -> None:
+def expert_decode(record: torch.Tensor, counts, table: bytes, out: torch.Tensor,
+                  stream: torch.cuda.Stream | None = None) -> None:
     """out (bf16, on the device) <- the values of an exponent-coded expert
-    record (uint8, on the device; layout in specfit_amd.codec)."""
+    record (uint8, on the device; layout and ``counts`` = (n_second,
+    n_third, n_raw) as in specfit_amd.codec)."""
     _require_cuda("record", record, torch.uint8)
     _require_cuda("out", out, _BF16)
     if record.dim() != 1 or not record.is_contiguous() or not out.is_contiguous():
         raise ValueError("expert_decode needs a contiguous 1-D record and a contiguous output")
     if len(table) != 32:
         raise ValueError("the exponent table has 32 entries")
+    if len(counts) != 3:
+        raise ValueError("counts are (n_second, n_third, n_raw)")
     tbl = (ctypes.c_uint8 * 32).from_buffer_copy(bytes(table))
+    n2, n3, nr = (int(c) for c in counts)
     rc = _native.lib().sf_expert_decode(_ptr(record), record.numel(), out.numel(), tbl,
-                                        int(n_secondary), int(n_raw), _ptr(out),
-                                        _stream_handle(stream, out.device))
+                                        n2, n3, nr, _ptr(out), _stream_handle(stream, out.device))
     _native.check(rc, "sf_expert_decode")
 
 

@@ -339,14 +339,14 @@ class GpuExpertCache:
         self._codec = compressed_sources
         # the (event, stream) after the decode that last read each staging buffer
         self._staging_reader: list = [None] * len(self._staging)
-        # Per coded expert: (record pointer, bytes, secondary and raw counts,
-        # ctypes exponent table), checked here once instead of per transfer.
+        # Per coded expert: (record pointer, bytes, list counts, ctypes
+        # exponent table), checked here once instead of per transfer.
         self._coded_args: dict = {}
         if compressed_sources is not None:
             blob = compressed_sources.blob.data_ptr()
             for key, r in compressed_sources.records.items():
                 if not r.raw:
-                    self._coded_args[key] = (blob + r.offset, r.nbytes, r.n_secondary, r.n_raw,
+                    self._coded_args[key] = (blob + r.offset, r.nbytes, tuple(r.counts),
                                              (ctypes.c_uint8 * 32).from_buffer_copy(r.table))
         self._staging_ptrs = [b.data_ptr() for b in self._staging]
         self.h2d_bytes = 0  # bytes moved over the host link
@@ -948,8 +948,8 @@ class GpuExpertCache:
             stream.wait_event(slot.ready_event)
         for guard in readers:
             self._await_reader(stream, guard)
-        ops.decode_staged(self._staging_ptrs[j], record[1], slot.tensor.numel(), record[4],
-                          record[2], record[3], slot.tensor.data_ptr(), stream)
+        ops.decode_staged(self._staging_ptrs[j], record[1], slot.tensor.numel(), record[3],
+                          record[2], slot.tensor.data_ptr(), stream)
 
     @staticmethod
     def _await_reader(stream: torch.cuda.Stream, guard: torch.cuda.Event) -> None:

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_error_strings():
-    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 11
+    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 12
     assert _native.error_string(0) == "success"
     assert _native.error_string(1) == "invalid argument"
     assert _native.error_string(12345) != ""

@@ -23,10 +23,10 @@ H, I, E, K = 2048, 768, 128, 8
 
 
 def _decode(values: torch.Tensor, force: bool = False) -> torch.Tensor:
-    rec, q, r, table = encode_record(values, force=force)
+    rec, counts, table = encode_record(values, force=force)
     assert rec is not None
     out = torch.full_like(values, float("nan"))
-    ops.expert_decode(rec, q, r, table, out)
+    ops.expert_decode(rec, counts, table, out)
     torch.cuda.synchronize()
     return out
 
@@ -38,10 +38,10 @@ def _same_bits(a: torch.Tensor, b: torch.Tensor) -> bool:
 def test_decode_restores_an_expert_at_the_real_size(device):
     g = torch.Generator(device=device).manual_seed(0)
     values = (torch.randn(3 * I * H, generator=g, device=device) * 0.02).to(torch.bfloat16)
-    rec, q, r, _ = encode_record(values)
-    print(f"expert record: {rec.numel()} of {2 * values.numel()} bytes, {q} secondary, "
-          f"{r} raw", flush=True)
-    assert rec.numel() <= 0.70 * 2 * values.numel()
+    rec, counts, _ = encode_record(values)
+    print(f"expert record: {rec.numel()} of {2 * values.numel()} bytes, counts {tuple(counts)}",
+          flush=True)
+    assert rec.numel() <= 0.68 * 2 * values.numel()
     assert _same_bits(_decode(values), values)
 
 
@@ -55,7 +55,7 @@ def test_decode_every_bit_pattern(device):
 def test_decode_chunk_edges_and_tails(device, n):
     g = torch.Generator(device=device).manual_seed(n)
     values = (torch.randn(n, generator=g, device=device) * 0.02).to(torch.bfloat16)
-    # rare exponents (secondary and raw codes) on both sides of every chunk
+    # rare exponents (level-3 and raw codes) on both sides of every chunk
     # edge and at the ends
     rare = torch.tensor([3.0e38, -1.0e-30, 0.0, float("inf"), 1.0e-12, 7.0, -3.0e-20, 2.0e10],
                         device=device).to(torch.bfloat16)
@@ -66,16 +66,18 @@ def test_decode_chunk_edges_and_tails(device, n):
 
 def test_decode_rejects_short_or_misaligned_records(device):
     values = torch.ones(4096, dtype=torch.bfloat16, device=device)
-    rec, q, r, table = encode_record(values, force=True)
+    rec, counts, table = encode_record(values, force=True)
     out = torch.empty_like(values)
     with pytest.raises(RuntimeError, match="invalid argument"):
-        ops.expert_decode(rec[:-256], q, r, table, out)
+        ops.expert_decode(rec[:-256], counts, table, out)
     with pytest.raises(RuntimeError, match="invalid argument"):
-        ops.expert_decode(rec, 1, 2, table, out)  # more raw than secondary entries
+        ops.expert_decode(rec, (1, 2, 0), table, out)  # more level-3 than level-2 entries
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        ops.expert_decode(rec, (2, 1, 2), table, out)  # more raw than level-3 entries
     shifted = torch.zeros(rec.numel() + 16, dtype=torch.uint8, device=device)
     shifted[1:1 + rec.numel()] = rec
     with pytest.raises(RuntimeError, match="misaligned"):
-        ops.expert_decode(shifted[1:], q, r, table, out)
+        ops.expert_decode(shifted[1:], counts, table, out)
 
 
 @pytest.fixture(scope="module")
@@ -103,10 +105,10 @@ def _layer(device, packed, router_w, slots, image=None):
 
 def test_coded_cache_matches_the_raw_cache(device, zipf_sources):
     """64-token Zipf steps through a 24-slot layer: the coded cache gives the
-    same outputs, counters and slot bytes as the raw one, with ~75% of the
+    same outputs, counters and slot bytes as the raw one, with ~67% of the
     bytes over the link."""
     packed, router_w, image = zipf_sources
-    assert image.transfer_bytes <= 0.70 * image.raw_bytes
+    assert image.transfer_bytes <= 0.68 * image.raw_bytes
     runs = []
     for coded in (False, True):
         router, cache, experts = _layer(device, packed, router_w, 24, image if coded else None)
@@ -124,7 +126,7 @@ def test_coded_cache_matches_the_raw_cache(device, zipf_sources):
     assert s_raw == s_cod and r_raw == r_cod and s_raw.h2d_submissions > 24
     assert all(torch.equal(a, b) for a, b in zip(o_raw, o_cod))
     assert _same_bits(st_raw, st_cod)
-    assert b_cod < 0.70 * b_raw
+    assert b_cod < 0.68 * b_raw
 
 
 def test_coded_cache_under_copy_stream_switches(device, zipf_sources):
