@@ -75,7 +75,7 @@ def parse_args():
                         "on the device; the slot holds the same bytes), or its raw bf16 bytes")
     p.add_argument("--expert-sets", type=int, default=24,
                    help="48-layer forwards: distinct pinned expert sets (1.125 GiB each); layer l "
-                        "copies its misses from set l mod N.  The GPU boxes this was measured on "
+                        "copies its misses from set l mod N.  The MI355X machines measured here "
                         "cap page-locked memory at ~36 GiB per process, so 48 distinct sets "
                         "(54 GiB) do not fit")
     p.add_argument("--shared-experts", action="store_true",

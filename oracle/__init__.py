@@ -1,8 +1,8 @@
 """CPU oracle of the offloaded Qwen3-MoE verification path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
-the ``cpu_baseline`` leg of ``bench.py`` may import this package, and only as
-the checker (or as the timed CPU baseline).  The product path
+the ``cpu_baseline`` leg of ``bench.py`` may import this package, and only to
+check results (or as the timed CPU baseline).  The product path
 (``specfit_amd``) never imports it and fails loudly when its HIP library is
 missing.
 

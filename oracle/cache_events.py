@@ -1,7 +1,7 @@
 """Independent replay of recorded cache transitions.
 
-TEST INFRASTRUCTURE ONLY (see the package docstring): the checker of the
-cross-layer prefetch audit.  It restates the event audit of
+TEST INFRASTRUCTURE ONLY (see the package docstring): the independent side
+of the cross-layer prefetch audit.  It restates the event audit of
 src/specfit/cross_layer_prefetch.py:60-142 (``CompactTransitions`` and
 ``replay_events``): starting from a logical pre-state of every layer cache
 (slots, LRU and submission sequences, counters, as read from snapshots), it

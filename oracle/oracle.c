@@ -1,8 +1,8 @@
 /*
  * CPU oracle for the offloaded Qwen3-MoE verification path -- TEST
  * INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg may load this library, and only as the checker (or the
- * timed CPU baseline); the product path never calls it.
+ * cpu_baseline leg may load this library, and only to check results (or as
+ * the timed CPU baseline); the product path never calls it.
  *
  * Bit-exact restatement of the integer/byte parts and of the router:
  *   oracle_router    tf:258-267 (Qwen3MoeTopKRouter.forward), with the fp32

@@ -19,7 +19,7 @@ Policy (the reference's, gpu_expert_cache.py:195-266, 495-609, 684-718):
   stream that read it (use guards recorded at release);
 * transfers become resident only when reaped, strictly in submission order.
 
-How this build holds that state:
+How the state is held here:
 
 * Device: one contiguous ``[slot_count, expert_numel]`` bf16 tensor, so a
   slot is a 9 MiB row the grouped SwiGLU kernel addresses as

@@ -27,7 +27,7 @@ Policy (the reference's):
 * with ``eviction_policy="probability"``, a speculative copy only replaces
   a writable victim of strictly lower predicted probability.
 
-How this build runs it (MI355X host path):
+How it runs here (MI355X host path):
 
 * The shared copy queue is a pair of SDMA streams that the caches
   alternate over (consecutive copies overlap one engine's setup with the

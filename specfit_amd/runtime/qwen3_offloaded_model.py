@@ -274,7 +274,7 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
     ``packed_checkpoint_root`` the experts and non-experts come from that
     packed-v1 checkpoint instead, validated against ``model_root``'s
     config/index hashes (the weight shards need not exist).
-    ``compress_expert_sources`` (an extension of this build): every layer's
+    ``compress_expert_sources`` (an extension beyond the reference): every layer's
     misses move exponent-coded records (specfit_amd.codec) over the host
     link and are decoded into the slots, which hold the same bytes."""
     from accelerate import init_empty_weights

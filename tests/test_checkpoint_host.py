@@ -2,7 +2,7 @@
 
 Restates the reference's tests (tests/unit/test_qwen3_packed_checkpoint.py:
 the same fixture checkpoint of 2 layers x 2 experts, hidden 2, intermediate
-3, split over two shards) for this build's writer and reader, plus the
+3, split over two shards) for specfit_amd.checkpoint's writer and reader, plus the
 direct pinned-layer reader.
 """
 import hashlib

@@ -4,7 +4,7 @@ Restates the reference's scheduler tests
 (tests/gpu/test_qwen3_expert_prefetch.py:77-440) and loader tests
 (tests/gpu/test_qwen3_offloaded_model.py:154-272) for this runtime.  Where
 the reference compares the offloaded model with HF eager bitwise (same
-cuBLAS kernels), this build compares within the MoE tolerance: its expert
+cuBLAS kernels), these tests compare within the MoE tolerance: the expert
 GEMMs and combine are different kernels.
 """
 import json
