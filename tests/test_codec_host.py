@@ -9,8 +9,9 @@ import pytest
 import torch
 
 from specfit_amd import _native
-from specfit_amd.codec import (CompressedExperts, decode_record_reference, encode_record,
-                               record_bytes, section_offsets)
+from specfit_amd.codec import CompressedExperts, encode_record, record_bytes, section_offsets
+
+from codec_reference import decode_record_reference
 
 
 def _bits(t: torch.Tensor) -> np.ndarray:
