@@ -172,3 +172,50 @@ def test_coded_decode_waits_for_the_slot_reader(device, zipf_sources):
     assert _same_bits(new, packed[8].to(device))
     assert cache.stats().h2d_submissions == 2 and cache.stats().evictions == 1
     cache.close()
+
+
+def test_loader_with_coded_sources_matches_raw_bit_for_bit(device):
+    """load_offloaded_qwen3(compress_expert_sources=True) on a small
+    Qwen3-MoE checkpoint (experts of 3 x 256 x 128 values, large enough to
+    code): the same logits as the raw loader bit for bit, under the
+    per-layer path and the prefetch scheduler, with fewer bytes over the
+    link and the same cache counters."""
+    import tempfile
+
+    from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
+
+    from specfit_amd.runtime import load_offloaded_qwen3
+    from test_gpu_prefetch_model import _save_qwen3_style_checkpoint
+
+    config = Qwen3MoeConfig(dtype=torch.bfloat16, vocab_size=64, hidden_size=256,
+                            intermediate_size=384, moe_intermediate_size=128,
+                            num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                            head_dim=64, num_experts=8, num_experts_per_tok=2,
+                            max_position_embeddings=64, bos_token_id=1, eos_token_id=2,
+                            pad_token_id=0, use_cache=True)
+    torch.manual_seed(4242)
+    source = Qwen3MoeForCausalLM(config).to(torch.bfloat16)
+    ids = torch.tensor([[1, 7, 11, 19, 23, 42]], device=device)
+    runs = []
+    with tempfile.TemporaryDirectory() as root:
+        _save_qwen3_style_checkpoint(source, root)
+        for coded in (False, True):
+            with load_offloaded_qwen3(root, device=device, slots_per_layer=3,
+                                      compress_expert_sources=coded) as loaded:
+                with torch.inference_mode():
+                    logits = [loaded.model(ids, use_cache=False).logits]
+                    loaded.cold_reset_expert_caches()
+                    with loaded.prefetch_experts({}, lookahead_layers=1) as sched:
+                        logits.append(loaded.model(ids, use_cache=False).logits)
+                    assert sched.stats()["complete"]
+                torch.cuda.synchronize()
+                moved = sum(c.h2d_bytes for c in loaded.expert_caches)
+                runs.append((logits, moved, loaded.layer_cache_stats()))
+    (raw_logits, raw_bytes, raw_stats), (cod_logits, cod_bytes, cod_stats) = runs
+    print(f"loader: {cod_bytes} of {raw_bytes} bytes over the link coded", flush=True)
+    assert all(torch.equal(a, b) for a, b in zip(raw_logits, cod_logits))
+    assert torch.equal(raw_logits[0], raw_logits[1])
+    counters = lambda stats: [(s.h2d_submissions, s.resident_hits, s.inflight_joins, s.evictions)
+                              for s in stats]
+    assert counters(raw_stats) == counters(cod_stats) and raw_bytes > 0
+    assert cod_bytes < 0.75 * raw_bytes
