@@ -121,9 +121,9 @@ __device__ __forceinline__ uint64_t read_bits(const uint32_t* w, int64_t bit0, i
 __device__ __forceinline__ void chunk_range(const uint32_t* table, int count, int chunk,
                                             int& first, int& last) {
   first = last = 0;
-  if (count > 0) {
-    first = min(static_cast<int>(table[chunk]), count);
-    last = min(static_cast<int>(table[chunk + 1]), count);
+  if (count > 0) {  // clamped as unsigned: an entry above INT_MAX is no negative rank
+    first = static_cast<int>(min(table[chunk], static_cast<uint32_t>(count)));
+    last = static_cast<int>(min(table[chunk + 1], static_cast<uint32_t>(count)));
   }
 }
 

@@ -80,6 +80,33 @@ def test_decode_rejects_short_or_misaligned_records(device):
         ops.expert_decode(shifted[1:], counts, table, out)
 
 
+def test_decode_of_a_malformed_record_reads_only_its_lists(device):
+    """Garbage chunk tables (entries up to 0xFFFFFFFF) and code bytes with
+    consistent counts: the decode clamps every rank to its list, so it
+    only reads inside the record, and each value keeps its own sign and
+    mantissa byte; only exponents can come out wrong."""
+    from specfit_amd.codec import section_offsets
+
+    g = torch.Generator(device=device).manual_seed(21)
+    values = (torch.randn(3 * 4096 + 77, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    rec, counts, table = encode_record(values, force=True)
+    off = section_offsets(values.numel(), counts)
+    h = torch.Generator().manual_seed(22)
+    for key, nxt in (("C2", "C3"), ("C3", "CR"), ("CR", "size")):
+        entries = torch.randint(0, 2**32, ((off[nxt] - off[key]) // 4,), generator=h,
+                                dtype=torch.int64)
+        entries[::2] = 0xFFFFFFFF
+        rec[off[key]:off[nxt]] = entries.to(torch.int32).view(torch.uint8).to(device)
+    n_codes = off["C2"] - off["L2"]
+    rec[off["L2"]:off["C2"]] = torch.randint(0, 256, (n_codes,), generator=h,
+                                             dtype=torch.int32).to(torch.uint8).to(device)
+    out = torch.empty_like(values)
+    ops.expert_decode(rec, counts, table, out)
+    torch.cuda.synchronize()
+    keep = lambda t: t.view(torch.int16) & 0x807F
+    assert torch.equal(keep(out), keep(values))
+
+
 @pytest.fixture(scope="module")
 def zipf_sources(device):
     packed = make_layer_sources(1, device=device, seed=11)[0]
