@@ -180,8 +180,10 @@ int sf_grouped_swiglu(const void *hidden, const int32_t *perm_pos,
  * K3, device slot-table form: computes every expert e < num_experts whose
  * slot_of_expert[e] >= 0 and that has at least one row, reading its weights
  * at slot_base + slot_of_expert[e] * slot_stride_elems (bf16 elements).
- * slot_of_expert is a device int32 [num_experts] array.  Needs no host-side
- * knowledge of which experts are active (no device-to-host read).
+ * slot_of_expert is a device int32 [num_experts] array whose entries are -1
+ * or the index of a slot behind slot_base (the kernel trusts them, as it
+ * trusts slot_base itself).  Needs no host-side knowledge of which experts
+ * are active (no device-to-host read).
  * max_rows bounds the rows of any expert as for sf_grouped_swiglu (tokens
  * is one when every token's top_k experts are distinct, as a router's are).
  */
