@@ -17,6 +17,11 @@ offloaded-model test compares against HF eager
   emptied first): forward hooks capture every layer's router input and
   output and every MoE block's input and output; routing is checked on all
   48 layers, the MoE output on four.
+
+The layer configurations run with raw transfers and with exponent-coded
+records (the benchmark default): both must meet the oracle, and give the
+same bits.  The 48-layer forward with coded records must reproduce the raw
+forward's routing and MoE outputs bit for bit on every layer.
 """
 from __future__ import annotations
 
@@ -28,6 +33,7 @@ import torch
 
 import oracle
 from specfit_amd import ops
+from specfit_amd.codec import CompressedExperts
 from specfit_amd.runtime import (ExpertKey, GpuExpertCache, Qwen3MoeTopKRouterHip,
                                  Qwen3OffloadedExperts)
 from specfit_amd.workloads import make_hidden, make_layer
@@ -65,6 +71,13 @@ def zipf_layer():
     return layer, _Fp32Experts(layer.experts)
 
 
+@pytest.fixture(scope="module")
+def zipf_image(device, zipf_layer):
+    layer, _ = zipf_layer
+    return CompressedExperts.encode({ExpertKey(0, e): layer.experts[e] for e in range(E)},
+                                    device=device)
+
+
 def _check_routing(hidden, router_weight, logits, w, idx, where: str):
     o_logits, o_w, o_idx, _ = oracle.router(_bits(hidden), _bits(router_weight), K, True)
     assert np.array_equal(_bits(logits), o_logits), f"{where}: logits differ from the oracle"
@@ -87,13 +100,14 @@ def _check_moe(hidden, idx, w_bits, out, experts32, where: str, *, bf16_check: b
     return err
 
 
-def _layer_modules(device, layer, slots: int):
+def _layer_modules(device, layer, slots: int, image=None):
     router = Qwen3MoeTopKRouterHip(num_experts=E, hidden_size=H, top_k=K, norm_topk_prob=True,
                                    device=device)
     with torch.no_grad():
         router.weight.copy_(layer.router)
     cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(E)},
-                           slot_count=slots, device=device, adopt_pinned_sources=True)
+                           slot_count=slots, device=device, adopt_pinned_sources=True,
+                           compressed_sources=image)
     experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H, intermediate_size=I,
                                     execution_policy="resident_first", h2d_prefetch=True)
     return router, cache, experts
@@ -131,8 +145,9 @@ def test_c1_resident16_slot_table_layer(device, uniform_layer):
         cache.close()
 
 
-def _prewarmed_forward(device, layer, *, tokens: int, slots: int, prewarm: int, seed0: int):
-    router, cache, experts = _layer_modules(device, layer, slots)
+def _prewarmed_forward(device, layer, *, tokens: int, slots: int, prewarm: int, seed0: int,
+                       image=None):
+    router, cache, experts = _layer_modules(device, layer, slots, image)
     for i in range(prewarm):
         h = make_hidden(tokens, seed=seed0 + i, zipf_fold=True).to(device)
         _, w, idx = router(h)
@@ -149,10 +164,21 @@ def _prewarmed_forward(device, layer, *, tokens: int, slots: int, prewarm: int, 
     return h, logits, w, idx, out, after.h2d_submissions - before.h2d_submissions
 
 
-def test_c2_layer_64_tokens_24_slots_zipf(device, zipf_layer):
+def _raw_and_coded(device, layer, image, where: str, **kwargs):
+    """The same prewarmed forward with raw transfers and with coded
+    records: identical routing, misses and output bits."""
+    raw = _prewarmed_forward(device, layer, **kwargs)
+    coded = _prewarmed_forward(device, layer, image=image, **kwargs)
+    for a, b in zip(raw[:5], coded[:5]):
+        assert torch.equal(a, b), f"{where}: coded transfers changed the forward"
+    assert raw[5] == coded[5]
+    return coded
+
+
+def test_c2_layer_64_tokens_24_slots_zipf(device, zipf_layer, zipf_image):
     layer, experts32 = zipf_layer
-    h, logits, w, idx, out, misses = _prewarmed_forward(device, layer, tokens=64, slots=24,
-                                                        prewarm=4, seed0=1)
+    h, logits, w, idx, out, misses = _raw_and_coded(device, layer, zipf_image, "C2", tokens=64,
+                                                    slots=24, prewarm=4, seed0=1)
     print(f"C2: {misses} misses in the measured forward", flush=True)
     assert misses > 0  # the miss path (H2D + per-group launches) is exercised
     o_idx, o_w = _check_routing(h, layer.router, logits, w, idx, "C2")
@@ -160,10 +186,11 @@ def test_c2_layer_64_tokens_24_slots_zipf(device, zipf_layer):
 
 
 @pytest.mark.parametrize("tokens", [1, 8, 32, 64, 128])
-def test_c3_sweep_12_slots_zipf(device, zipf_layer, tokens):
+def test_c3_sweep_12_slots_zipf(device, zipf_layer, zipf_image, tokens):
     layer, experts32 = zipf_layer
-    h, logits, w, idx, out, misses = _prewarmed_forward(device, layer, tokens=tokens, slots=12,
-                                                        prewarm=2, seed0=100 + tokens)
+    h, logits, w, idx, out, misses = _raw_and_coded(device, layer, zipf_image, f"C3 T={tokens}",
+                                                    tokens=tokens, slots=12, prewarm=2,
+                                                    seed0=100 + tokens)
     print(f"C3 T={tokens}: {misses} misses", flush=True)
     o_idx, o_w = _check_routing(h, layer.router, logits, w, idx, f"C3 T={tokens}")
     _check_moe(h, o_idx, o_w, out, experts32, f"C3 T={tokens}")
@@ -263,3 +290,41 @@ def test_c5_cold48_routing_every_layer_and_moe_outputs(device, verify_model):
     print(f"C5: misses per layer min {min(misses)} max {max(misses)}", flush=True)
     assert min(misses) >= 100  # nearly every expert of every layer copied in
     _check_48_layers(loaded, captured, experts32, 128, "C5")
+
+
+def test_c4_verify48_coded_transfers_reproduce_raw_bit_for_bit(device, verify_model,
+                                                                 uniform_layer):
+    """The 48-layer verification forward with exponent-coded records (the
+    benchmark default): the same routing, MoE inputs and MoE outputs as the
+    raw-transfer model on every layer, bit for bit, from empty caches."""
+    from specfit_amd.runtime import synthetic_tree
+    from specfit_amd.workloads import make_kv_context, make_verify_model
+
+    raw, raw_cache, _ = verify_model
+    layer, _ = uniform_layer
+    coded = make_verify_model(device=device, layers=48, slots_per_layer=12, experts=layer,
+                              compress_expert_sources=True)
+    try:
+        coded_cache = make_kv_context(coded.model.config, 1024, device=device, seed=1)
+        tree = synthetic_tree(60, 6, seed=300, vocab=coded.model.config.vocab_size)
+        seed_token = torch.tensor([[29]], device=device)
+        runs = []
+        for loaded, kv in ((raw, raw_cache), (coded, coded_cache)):
+            torch.cuda.synchronize()
+            loaded.cold_reset_expert_caches()
+            before = sum(c.h2d_bytes for c in loaded.expert_caches)
+            captured = _captured_forward(loaded, kv, tree, seed_token)
+            kv.crop(1024)
+            moved = sum(c.h2d_bytes for c in loaded.expert_caches) - before
+            runs.append((captured, moved, [c.stats().h2d_submissions
+                                           for c in loaded.expert_caches]))
+        (c_raw, b_raw, m_raw), (c_cod, b_cod, m_cod) = runs
+        print(f"C4 coded: {b_cod} of {b_raw} bytes over the link", flush=True)
+        assert b_cod < 0.70 * b_raw
+        for part in range(1, 5):  # gate in/out, MoE in/out of every layer
+            for lid in range(48):
+                a, b = c_raw[part][lid], c_cod[part][lid]
+                pairs = zip(a, b) if isinstance(a, tuple) else [(a, b)]
+                assert all(torch.equal(x, y) for x, y in pairs), f"layer {lid} part {part}"
+    finally:
+        coded.close()
