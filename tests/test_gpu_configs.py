@@ -12,6 +12,8 @@ offloaded-model test compares against HF eager
   slot-table forward (asserted to be the path taken);
 * 64 tokens, 24-slot LRU cache, Zipf(1.1) routing after pre-warm cycles;
 * 1 / 8 / 32 / 64 / 128 tokens with a 12-slot cache, Zipf routing;
+* 16 and 64 tokens through an 8-slot cache of 32 experts of the
+  Qwen3-235B-A22B expert shape (hidden 4096, intermediate 1536);
 * the 48-layer verification forward (60-node tree over a 1024-token
   context, 12 slots per layer) and the cold 128-token forward (every cache
   emptied first): forward hooks capture every layer's router input and
@@ -78,38 +80,42 @@ def zipf_image(device, zipf_layer):
                                     device=device)
 
 
-def _check_routing(hidden, router_weight, logits, w, idx, where: str):
-    o_logits, o_w, o_idx, _ = oracle.router(_bits(hidden), _bits(router_weight), K, True)
+def _check_routing(hidden, router_weight, logits, w, idx, where: str, k: int = K):
+    o_logits, o_w, o_idx, _ = oracle.router(_bits(hidden), _bits(router_weight), k, True)
     assert np.array_equal(_bits(logits), o_logits), f"{where}: logits differ from the oracle"
     assert np.array_equal(idx.cpu().numpy(), o_idx), f"{where}: indices differ from the oracle"
     assert np.array_equal(_bits(w), o_w), f"{where}: weights differ from the oracle"
     return o_idx, o_w
 
 
-def _check_moe(hidden, idx, w_bits, out, experts32, where: str, *, bf16_check: bool = True):
+def _check_moe(hidden, idx, w_bits, out, experts32, where: str, *, bf16_check: bool = True,
+               shape: tuple = (H, I, E)):
+    h_, i_, e_ = shape
     x = oracle.bf16_float(_bits(hidden))
     wf = oracle.bf16_float(w_bits)
-    y32 = oracle.moe_forward_fp32(x, idx, wf, experts32, H, I)
+    y32 = oracle.moe_forward_fp32(x, idx, wf, experts32, h_, i_)
     got = oracle.bf16_float(_bits(out))
     err = float(np.abs(got - y32).max() / np.abs(y32).max())
     print(f"{where}: MoE max normalised error vs fp32 oracle {err:.3e}", flush=True)
     assert err <= 1e-2, f"{where}: error {err:.3e} above 1e-2"
     if bf16_check:
-        yb = oracle.moe_forward_bf16(x, idx, wf, experts32, H, I, E, accumulate_fp32=True)
+        yb = oracle.moe_forward_bf16(x, idx, wf, experts32, h_, i_, e_, accumulate_fp32=True)
         np.testing.assert_allclose(got, yb, rtol=1.6e-2, atol=1.6e-2, err_msg=where)
     return err
 
 
 def _layer_modules(device, layer, slots: int, image=None):
-    router = Qwen3MoeTopKRouterHip(num_experts=E, hidden_size=H, top_k=K, norm_topk_prob=True,
-                                   device=device)
+    h_, i_, e_ = layer.hidden_size, layer.intermediate_size, layer.experts.shape[0]
+    router = Qwen3MoeTopKRouterHip(num_experts=e_, hidden_size=h_, top_k=layer.top_k,
+                                   norm_topk_prob=True, device=device)
     with torch.no_grad():
         router.weight.copy_(layer.router)
-    cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(E)},
+    cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(e_)},
                            slot_count=slots, device=device, adopt_pinned_sources=True,
                            compressed_sources=image)
-    experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H, intermediate_size=I,
-                                    execution_policy="resident_first", h2d_prefetch=True)
+    experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=h_,
+                                    intermediate_size=i_, execution_policy="resident_first",
+                                    h2d_prefetch=True)
     return router, cache, experts
 
 
@@ -148,13 +154,14 @@ def test_c1_resident16_slot_table_layer(device, uniform_layer):
 def _prewarmed_forward(device, layer, *, tokens: int, slots: int, prewarm: int, seed0: int,
                        image=None):
     router, cache, experts = _layer_modules(device, layer, slots, image)
+    width = layer.hidden_size
     for i in range(prewarm):
-        h = make_hidden(tokens, seed=seed0 + i, zipf_fold=True).to(device)
+        h = make_hidden(tokens, width, seed=seed0 + i, zipf_fold=True).to(device)
         _, w, idx = router(h)
         experts(h, idx, w)
     torch.cuda.synchronize()
     before = cache.stats()
-    h = make_hidden(tokens, seed=seed0 + prewarm, zipf_fold=True).to(device)
+    h = make_hidden(tokens, width, seed=seed0 + prewarm, zipf_fold=True).to(device)
     logits, w, idx = router(h)
     out = experts(h, idx, w)
     torch.cuda.synchronize()
@@ -194,6 +201,38 @@ def test_c3_sweep_12_slots_zipf(device, zipf_layer, zipf_image, tokens):
     print(f"C3 T={tokens}: {misses} misses", flush=True)
     o_idx, o_w = _check_routing(h, layer.router, logits, w, idx, f"C3 T={tokens}")
     _check_moe(h, o_idx, o_w, out, experts32, f"C3 T={tokens}")
+
+
+# ------------------------------------------- Qwen3-235B-A22B expert shape --
+@pytest.fixture(scope="module")
+def layer_235b(device):
+    """32 experts of the Qwen3-235B-A22B shape (hidden 4096, intermediate
+    1536: 37.7 MB each) in page-locked memory, a router and their records."""
+    from specfit_amd.workloads import MoELayerWeights, make_layer_sources
+
+    h_, i_, e_ = 4096, 1536, 32
+    packed = make_layer_sources(1, device=device, seed=5, hidden_size=h_, num_experts=e_,
+                                intermediate_size=i_)[0]
+    g = torch.Generator().manual_seed(6)
+    router = (torch.randn(e_, h_, generator=g) * 0.02).to(torch.bfloat16)
+    layer = MoELayerWeights(router, packed, h_, i_, K, None)
+    image = CompressedExperts.encode({ExpertKey(0, e): packed[e] for e in range(e_)},
+                                     device=device)
+    return layer, _Fp32Experts(packed), image
+
+
+@pytest.mark.parametrize("tokens", [16, 64])
+def test_qwen3_235b_expert_shape_layer(device, layer_235b, tokens):
+    """The larger expert shape through an 8-slot cache with misses, raw and
+    coded: routing bit-exact, MoE output against the oracle."""
+    layer, experts32, image = layer_235b
+    where = f"235B-shape T={tokens}"
+    h, logits, w, idx, out, misses = _raw_and_coded(device, layer, image, where, tokens=tokens,
+                                                    slots=8, prewarm=2, seed0=400 + tokens)
+    print(f"{where}: {misses} misses", flush=True)
+    assert misses > 0
+    o_idx, o_w = _check_routing(h, layer.router, logits, w, idx, where)
+    _check_moe(h, o_idx, o_w, out, experts32, where, shape=(4096, 1536, 32))
 
 
 # ------------------------------------------------------- 48-layer forwards --
