@@ -127,16 +127,34 @@ __device__ __forceinline__ void chunk_range(const uint32_t* table, int count, in
   }
 }
 
+// Bit j of n (n < 16) moved to bit 8 j: the multiplier's four terms put bit j
+// at j + 7 i, all distinct for i, j < 4, and only i = j lands on 8 j.
+__device__ __forceinline__ uint32_t spread4(uint32_t n) {
+  return __umul24(n, 0x00204081u) & 0x01010101u;
+}
+
+// Byte i of the result = byte sel_i of {hi (bytes 4..7) : lo (bytes 0..3)};
+// selector byte 12 gives 0.
+__device__ __forceinline__ uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
 // One workgroup per chunk; thread t decodes values 16 t .. 16 t + 15 of
 // it.  A value that reaches level 2 or 3 takes the code at its rank among
 // the chunk's values that reach that level, counted from the chunk's first
-// entry of that level's list; a raw exponent likewise.  Ranks come from workgroup
-// prefixes over per-thread counts (skipped for a list the chunk has no
-// entries of), so every value is written once.  Entries a malformed record
-// lacks count as the next level's escape; a value left without a raw byte
-// keeps exponent 0.
+// entry of that level's list; a raw exponent likewise.  Ranks come from
+// workgroup prefixes over per-thread counts (skipped for a list the chunk
+// has no entries of), so every value is written once.  Entries a malformed
+// record lacks count as the next level's escape; a value left without a raw
+// byte keeps exponent 0.
+//
+// Exponents of levels 1 and 2 come four values at a time from one byte
+// permute over table bytes 0..3 and 8..11: value j's selector is its level-1
+// code, or 4 + its level-2 code when the level-1 code is 3 (selector 7, a
+// level-3 value, is patched after).  Sign, exponent and mantissa bytes are
+// joined four values at a time: the low byte of a bf16 value is its mantissa
+// and exponent bit 0, the high byte its sign and exponent bits 1..7.
 __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
-  __shared__ uint8_t table[32];
   __shared__ int wave_total[3][kWaves];
   const int tid = threadIdx.x;
   const int chunk = blockIdx.x;
@@ -161,7 +179,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
   chunk_range(a.c2, a.n2, chunk, f2, l2);
   chunk_range(a.c3, a.n3, chunk, f3, l3);
   chunk_range(a.cr, a.nr, chunk, fr, lr);
-  if (tid < 32) table[tid] = static_cast<uint8_t>(a.table[tid >> 2] >> (8 * (tid & 3)));
 
   // Level 2: this thread's entries are consecutive in L2 from rank r2.
   const uint32_t esc1 = p0 & p1;
@@ -171,13 +188,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
   const int v2 = max(0, min(k1, l2 - r2));
   uint32_t codes2 = static_cast<uint32_t>(read_bits(a.l2, 2 * static_cast<int64_t>(r2), 2 * v2));
   if (v2 < k1) codes2 |= ~0u << (2 * v2);  // missing entries escape
-  const uint32_t at3 = codes2 & (codes2 >> 1) & 0x55555555u;  // bit 2j: entry j is code 3
-  uint32_t esc2 = 0;
-#pragma unroll
-  for (int k = 0; k < kPerThread; ++k) {
-    const int j = __popc(esc1 & ((1u << k) - 1));
-    esc2 |= ((esc1 >> k) & (at3 >> (2 * j)) & 1u) << k;
+  // Bit j of c2lo / c2hi: bit 0 / bit 1 of value j's level-2 code (0 for a
+  // value without one).
+  uint32_t c2lo = 0, c2hi = 0;
+  for (uint32_t m = esc1, c = codes2; m; m &= m - 1, c >>= 2) {
+    const uint32_t bit = m & (0u - m);
+    c2lo |= (c & 1u) ? bit : 0u;
+    c2hi |= (c & 2u) ? bit : 0u;
   }
+  const uint32_t esc2 = c2lo & c2hi;
 
   // Level 3: consecutive in L3 from rank r3.
   const int k2 = __popc(esc2);
@@ -186,36 +205,56 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
   const int v3 = max(0, min(k2, l3 - r3));
   uint64_t codes3 = read_bits(a.l3, 4 * static_cast<int64_t>(r3), 4 * v3);
   if (v3 < k2) codes3 |= ~uint64_t{0} << (4 * v3);
-  uint32_t esc3 = 0;
-#pragma unroll
-  for (int k = 0; k < kPerThread; ++k) {
-    const int j = __popc(esc2 & ((1u << k) - 1));
-    const uint32_t c = static_cast<uint32_t>(codes3 >> (4 * j)) & 15u;
-    esc3 |= static_cast<uint32_t>((esc2 >> k) & 1u & (c == 15u)) << k;
+  uint32_t esc3 = 0;  // values with a raw exponent
+  {
+    uint64_t c = codes3;
+    for (uint32_t m = esc2; m; m &= m - 1, c >>= 4)
+      if ((static_cast<uint32_t>(c) & 15u) == 15u) esc3 |= m & (0u - m);
   }
-
   // Raw exponents: consecutive in R from rank rr.
   int rr = fr;
   if (lr > fr) rr += workgroup_prefix(__popc(esc3), wave_total[2]);
-  __syncthreads();  // the table
 
+  uint32_t ew[4];  // exponent bytes of values 4w .. 4w+3
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t s1 = spread4((p0 >> (4 * w)) & 15u) | (spread4((p1 >> (4 * w)) & 15u) << 1);
+    const uint32_t s2 =
+        spread4((c2lo >> (4 * w)) & 15u) | (spread4((c2hi >> (4 * w)) & 15u) << 1);
+    const uint32_t to_level2 = s1 & (s1 >> 1) & 0x01010101u;  // level-1 code 3
+    ew[w] = byte_perm(a.table[2], a.table[0], s1 + to_level2 + s2);
+  }
+  // Level-3 and raw exponents, in value order.
+  {
+    uint64_t c = codes3;
+    int rank = rr;
+    for (uint32_t m = esc2; m; m &= m - 1, c >>= 4) {
+      const int k = __builtin_ctz(m);
+      const uint32_t code = static_cast<uint32_t>(c) & 15u;
+      uint32_t e;
+      if (code != 15u) {  // table[16 + code] into byte 0, zeros above
+        const uint32_t sel = 0x0c0c0c00u | (code & 7u);
+        e = code < 8u ? byte_perm(a.table[5], a.table[4], sel)
+                      : byte_perm(a.table[7], a.table[6], sel);
+      } else {
+        e = rank < lr ? a.raw[rank] : 0u;
+        ++rank;
+      }
+      const int sh = 8 * (k & 3);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t mask = (k >> 2) == w ? 0xffu << sh : 0u;
+        ew[w] = (ew[w] & ~mask) | ((e << sh) & mask);
+      }
+    }
+  }
   uint32_t w16[8];
 #pragma unroll
-  for (int k = 0; k < kPerThread; ++k) {
-    const uint32_t c1 = ((p0 >> k) & 1u) | (((p1 >> k) & 1u) << 1);
-    const int j2 = __popc(esc1 & ((1u << k) - 1));
-    const int j3 = __popc(esc2 & ((1u << k) - 1));
-    const uint32_t c2 = (codes2 >> (2 * j2)) & 3u;
-    const uint32_t c3 = static_cast<uint32_t>(codes3 >> (4 * j3)) & 15u;
-    const uint32_t idx = c1 != 3u ? c1 : (c2 != 3u ? 8u + c2 : 16u + c3);
-    uint32_t e = table[idx];
-    if ((esc3 >> k) & 1u) {
-      const int rank = rr + __popc(esc3 & ((1u << k) - 1));
-      e = rank < lr ? a.raw[rank] : 0u;
-    }
-    const uint32_t v = join((sw[k >> 2] >> (8 * (k & 3))) & 0xffu, e);
-    if (k & 1) w16[k >> 1] |= v << 16;
-    else w16[k >> 1] = v;
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t lo = (sw[w] & 0x7f7f7f7fu) | ((ew[w] << 7) & 0x80808080u);
+    const uint32_t hi = (sw[w] & 0x80808080u) | ((ew[w] >> 1) & 0x7f7f7f7fu);
+    w16[2 * w] = byte_perm(hi, lo, 0x05010400u);      // values 4w, 4w+1
+    w16[2 * w + 1] = byte_perm(hi, lo, 0x07030602u);  // values 4w+2, 4w+3
   }
   if (nv == kPerThread) {
     uint4* o = reinterpret_cast<uint4*>(a.out + i);
