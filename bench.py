@@ -11,7 +11,11 @@ forward of a fresh 64-token batch (router K1 -> dispatch K2 -> cache
 resolution + H2D -> grouped SwiGLU K3 -> combine K4), through the drop-in
 runtime API (Qwen3MoeTopKRouterHip + Qwen3OffloadedExperts with the
 resident-first policy and one-ahead prefetch).  Inputs are resident in HBM
-before the timed region; the timed region includes every H2D transfer.
+before the timed region; the timed region includes every H2D transfer.  By
+default a miss moves the expert's exponent-coded record (specfit_amd.codec,
+~67% of the bytes), decoded into the slot on the device, which then holds
+the raw bf16 bytes; --transfer raw moves the raw bytes, as the reference
+does.
 
 Every workload runs two passes of --steps steps.  The timed pass carries no
 timing events: `value` and `ms_per_step` come from it.  The recorded pass,
