@@ -195,7 +195,7 @@ class _RunPin:
 
     def __init__(self, cache: "GpuExpertCache", entries: tuple, readers: dict) -> None:
         self._cache = cache
-        self._entries = entries  # ((slot id, key, generation), ...)
+        self._entries = entries  # [(slot id, key, generation), ...]
         self._readers = readers
         self._state = _PINNED
 
@@ -571,11 +571,16 @@ class GpuExpertCache:
                         ev = events[sid] = torch.cuda.Event(blocking=False)
                         ev.record(stream)
                     guards.append((sid, ev))
+                # One loop per slot (the body of _check_pin inlined: this
+                # runs once per expert of every launch).
                 for slot_id, key, generation in pin._pinned_slots():
                     slot = slots[slot_id]
-                    self._check_pin(slot, key, generation)
+                    if ((slot.expert_id is not key and slot.expert_id != key)
+                            or slot.generation != generation or slot.active_leases <= 0):
+                        raise RuntimeError("expert lease refers to a reused GPU slot")
+                    use = slot.use_events
                     for sid, ev in guards:
-                        slot.use_events[sid] = ev
+                        use[sid] = ev
                     slot.active_leases -= 1
 
     # -------------------------------------------------- batched lease runs --
@@ -631,10 +636,10 @@ class GpuExpertCache:
         wait's deferred touch (all steps but a first one whose carried lease
         has none), release (touch, pin kept).  All slots of a run are
         distinct, so each ends at its release touch's sequence number."""
-        resident = self._resident
+        get = self._resident.get
         ids = []
         for k in keys[index:index + limit + 1]:
-            sid = resident.get(k)
+            sid = get(k)
             if sid is None:
                 break
             ids.append(sid)
@@ -661,17 +666,20 @@ class GpuExpertCache:
             current._state = _PINNED
             out.append((keys[index].expert_id, current, run[0].tensor))
             first_pinned = 1
-        if first_pinned < steps:
-            entries = tuple((run[j].slot_id, keys[index + j], run[j].generation)
-                            for j in range(first_pinned, steps))
-            pin = _RunPin(self, entries, {handle: stream})
-            out.extend((keys[index + j].expert_id, pin, run[j].tensor)
-                       for j in range(first_pinned, steps))
+        entries = []
+        pin = _RunPin(self, entries, {handle: stream}) if first_pinned < steps else None
         seq = self._sequence + fresh + deferred
+        # One pass per step: its touches, the next slot's pin, and (past a
+        # carried-in lease) the run pin's entry and the caller's step.
         for j in range(steps):
+            slot = run[j]
             seq += 2 if j else 1  # (the wait's deferred touch) + the release touch
-            run[j].last_used_sequence = seq
+            slot.last_used_sequence = seq
             run[j + 1].active_leases += 1
+            if j >= first_pinned:
+                key = keys[index + j]
+                entries.append((slot.slot_id, key, slot.generation))
+                out.append((key.expert_id, pin, slot.tensor))
         self._sequence = seq
         self._state_version += fresh + 3 * steps - 1 + deferred
         self._stats.resident_hits += fresh + steps

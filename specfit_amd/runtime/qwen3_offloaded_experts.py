@@ -179,11 +179,7 @@ class Qwen3OffloadedExperts(nn.Module):
         if routes is None:
             return torch.zeros_like(hidden_states)
         self._run_legacy(order, routes)
-        if self.reduction_mode is ReductionMode.ARRIVAL_ORDER:
-            return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
-                               expert_rank=self._arrival_ranks(order), accumulate_fp32=False)
-        return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
-                           accumulate_fp32=self.combine_fp32)
+        return self._combine_rows(routes, top_k_index, order)
 
     def _uses_slot_table(self) -> bool:
         """The resident-first, one-ahead forward with the stock K3 seam and a
@@ -246,16 +242,30 @@ class Qwen3OffloadedExperts(nn.Module):
                 entry[0] = len(routes.covered)
                 entry[1] = sum(counts[e] for e in routes.covered)
             order = self._resolve_execution_order(active, None)
+            if len(routes.covered) == len(active):
+                # The table launch computed every routed expert: the combine
+                # needs nothing from the lease sequence, so it is enqueued
+                # first and the host's bookkeeping (touches, counters, use
+                # guards, all recorded after the table launch on this
+                # stream) overlaps the device work instead of delaying it.
+                out = self._combine_rows(routes, top_k_index, order)
+                # Nothing is launched from this lease sequence, so the batch
+                # cap of K3 launches does not apply: one run, one unpin.
+                self._run_legacy(order, routes, batch_cap=len(order) + 1)
+                return out
             self._run_legacy(order, routes)
+        return self._combine_rows(routes, top_k_index, order)
+
+    def _combine_rows(self, routes, top_k_index, order) -> torch.Tensor:
         if self.reduction_mode is ReductionMode.ARRIVAL_ORDER:
             return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
                                expert_rank=self._arrival_ranks(order), accumulate_fp32=False)
         return ops.combine(routes.rows, top_k_index, routes.plan, self.hidden_size,
                            accumulate_fp32=self.combine_fp32)
 
-    def _run_legacy(self, order, routes) -> None:
+    def _run_legacy(self, order, routes, batch_cap: int = _MAX_BATCH) -> None:
         before = self.cache._stats.h2d_submissions
-        self._run_in_order(order, routes)
+        self._run_in_order(order, routes, batch_cap)
         self._last_forward_copied = self.cache._stats.h2d_submissions != before
 
     def _upload_slot_table(self, version: int | None, slots: list[int],
@@ -417,7 +427,8 @@ class Qwen3OffloadedExperts(nn.Module):
         finally:
             self.cache._unpin_many([lease for _, lease, _ in batch])
 
-    def _run_in_order(self, order: tuple[int, ...], routes: _GroupedRoutes) -> None:
+    def _run_in_order(self, order: tuple[int, ...], routes: _GroupedRoutes,
+                      batch_cap: int = _MAX_BATCH) -> None:
         """Reference lease sequence (acquire, optional one-ahead prefetch,
         wait, release) with the K3 launches batched.
 
@@ -425,7 +436,9 @@ class Qwen3OffloadedExperts(nn.Module):
         Pinned slots were all touched after every unpinned slot, so as long
         as one unleased, unpinned slot exists the LRU victim of the next
         miss is the same slot the reference would pick; otherwise the batch
-        is launched first.  Batches are also capped at ``_MAX_BATCH``."""
+        is launched first.  Batches are also capped at ``batch_cap``
+        (``_MAX_BATCH`` experts per K3 launch unless the caller knows that
+        no batch launches anything)."""
         cache = self.cache
         stream = torch.cuda.current_stream(cache.device)
         batch: list[tuple[int, ExpertLease, torch.Tensor]] = []
@@ -464,10 +477,10 @@ class Qwen3OffloadedExperts(nn.Module):
                     # Runs of resident experts: the same lease sequence in
                     # one locked pass (no miss can occur inside the run).
                     steps, index, ahead = cache._resident_steps(keys, index, ahead, stream,
-                                                                _MAX_BATCH - len(batch))
+                                                                batch_cap - len(batch))
                     if steps:
                         batch.extend(steps)
-                        if len(batch) >= _MAX_BATCH:
+                        if len(batch) >= batch_cap:
                             flush()
                         continue
                 expert_id = order[index]
@@ -494,7 +507,7 @@ class Qwen3OffloadedExperts(nn.Module):
                 batch.append((expert_id, current, weights))
                 current._release_keep_pinned()
                 misses += int(missed)
-                if (len(batch) >= _MAX_BATCH or misses >= miss_group
+                if (len(batch) >= batch_cap or misses >= miss_group
                         or (misses == 0 and ahead_missed)):
                     flush()
             flush()
