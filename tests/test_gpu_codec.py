@@ -45,6 +45,34 @@ def test_decode_restores_an_expert_at_the_real_size(device):
     assert _same_bits(_decode(values), values)
 
 
+def test_decode_restores_an_expert_of_the_larger_shape(device):
+    """The Qwen3-235B-A22B expert (3 x 1536 x 4096 values, 4,608 chunks)."""
+    g = torch.Generator(device=device).manual_seed(1)
+    values = (torch.randn(3 * 1536 * 4096, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    rec, counts, _ = encode_record(values)
+    assert rec is not None and rec.numel() <= 0.68 * 2 * values.numel()
+    assert _same_bits(_decode(values), values)
+
+
+@pytest.mark.parametrize("case", ["constant", "two exponents", "zeros and signs"])
+def test_decode_experts_with_few_exponents(device, case):
+    """Tables with unused entries: one value repeated, two binades, and
+    +-0 (exponent 0) mixed with one other value."""
+    n = 2 * 4096 + 333
+    g = torch.Generator(device=device).manual_seed(7)
+    if case == "constant":
+        values = torch.full((n,), -0.0234, device=device).to(torch.bfloat16)
+    elif case == "two exponents":
+        pick = torch.randint(0, 2, (n,), generator=g, device=device)
+        values = torch.where(pick == 1, 0.75, 1.5).to(torch.bfloat16)
+    else:
+        pick = torch.randint(0, 3, (n,), generator=g, device=device)
+        values = torch.where(pick == 0, 0.0, torch.where(pick == 1, -0.0, 3.0)).to(torch.bfloat16)
+    rec, counts, _ = encode_record(values, force=True)
+    assert tuple(counts) == (0, 0, 0)
+    assert _same_bits(_decode(values, force=True), values)
+
+
 def test_decode_every_bit_pattern(device):
     values = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16)
     values = values.view(torch.bfloat16)
