@@ -383,8 +383,8 @@ def main_verify(args) -> int:
                  + f"), random N(0,1) {args.context}-token KV context, seeded random trees"),
         "config": {"workload": (f"qwen3-30b-a3b verification forward, {args.layers} layers, "
                                 f"{args.tree_nodes}-node depth-{args.tree_depth} tree over a "
-                                f"{args.context}-token context, {args.verify_slots}-slot LRU expert "
-                                f"cache per layer" + (", caches emptied before every forward"
+                                f"{args.context}-token context, {args.verify_slots}-slot LRU "
+                                f"expert cache per layer" + (", caches emptied before every forward"
                                                       if cold else "")),
                    "layers": args.layers, "context": args.context, "tree_nodes": args.tree_nodes,
                    "tree_depth": args.tree_depth, "cache_slots": args.verify_slots,
@@ -590,7 +590,8 @@ def main() -> int:
                        pin_memory=True)
     H, I, E, K = layer.hidden_size, layer.intermediate_size, layer.num_experts, layer.top_k
     expert_bytes = layer.expert_bytes
-    log(f"layer generated in {time.perf_counter() - t0:.1f}s ({E} experts x {expert_bytes} B pinned)")
+    log(f"layer generated in {time.perf_counter() - t0:.1f}s "
+        f"({E} experts x {expert_bytes} B pinned)")
 
     router = Qwen3MoeTopKRouterHip(num_experts=E, hidden_size=H, top_k=K, norm_topk_prob=True,
                                    device=dev)
@@ -809,7 +810,8 @@ def main() -> int:
         "overlap": overlap,
         "h2d_link_busy_frac": h2d_time / rec_wall if h2d_time else None,
         "decode": decode_stats(rec),
-        "k3_resident_in_step": {"launches": len(res), "gbs": res_bytes / res_time / 1e9 if res_time else None},
+        "k3_resident_in_step": {"launches": len(res),
+                                "gbs": res_bytes / res_time / 1e9 if res_time else None},
         "k3_all_resident": {"experts": len(active), "rows": rows_n, "us": res_launch * 1e6,
                             "gbs": res_launch_bytes / res_launch / 1e9,
                             "frac": res_launch_bytes / res_launch / 1e9 / HBM_PEAK_GBS},

@@ -261,7 +261,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     o[0] = make_uint4(w16[0], w16[1], w16[2], w16[3]);
     o[1] = make_uint4(w16[4], w16[5], w16[6], w16[7]);
   } else {
-    for (int k = 0; k < nv; ++k) a.out[i + k] = static_cast<uint16_t>(w16[k >> 1] >> (16 * (k & 1)));
+    for (int k = 0; k < nv; ++k)
+      a.out[i + k] = static_cast<uint16_t>(w16[k >> 1] >> (16 * (k & 1)));
   }
 }
 

@@ -525,7 +525,8 @@ def grouped_swiglu_table(hidden: torch.Tensor, plan: DispatchPlan,
 
 
 def expert_swiglu(rows: torch.Tensor, packed: torch.Tensor, hidden_size: int,
-                  intermediate_size: int, *, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+                  intermediate_size: int, *,
+                  stream: torch.cuda.Stream | None = None) -> torch.Tensor:
     """y = SwiGLU expert MLP of already-gathered rows (no routing weight)."""
     _require_cuda("hidden_states", rows, _BF16)
     _require_cuda("packed expert", packed, _BF16)

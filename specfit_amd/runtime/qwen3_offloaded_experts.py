@@ -169,7 +169,8 @@ class Qwen3OffloadedExperts(nn.Module):
         self._validate_inputs(hidden_states, top_k_index, top_k_weights)
         if self._prediction_scheduler is not None:
             if execution_order is not None:
-                raise ValueError("explicit execution_order conflicts with dynamic predicted prefetch")
+                raise ValueError(
+                    "explicit execution_order conflicts with dynamic predicted prefetch")
             return self._forward_prefetched(hidden_states, top_k_index, top_k_weights)
         if execution_order is None and self._uses_slot_table():
             return self._forward_slot_table(hidden_states, top_k_index, top_k_weights)
