@@ -562,6 +562,17 @@ def main() -> int:
               "(the verification path runs on a single MI355X; multi-GPU sharding is a "
               "design note, not a built path)", file=sys.stderr)
         return 2
+    import torch
+
+    # Verification needs no autograd: every workload runs under inference
+    # mode, as the reference's measured decode loop does
+    # (scripts/run_specfit_main_comparison.py:713).
+    with torch.inference_mode():
+        return main_workload(args)
+
+
+def main_workload(args) -> int:
+    """Run the workload ``args`` names and print its JSON line."""
     if args.workload in ("verify48", "cold48"):
         if args.workload == "cold48" and args.tree_nodes == 60:
             args.tree_nodes = 127  # 128 tree tokens
