@@ -67,7 +67,8 @@ def test_verification_shape_with_tree_mask(device):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 8), (4, 2, 8), (8, 2, 64), (16, 4, 128),
-                                      (16, 1, 128), (32, 4, 96), (8, 2, 256)])
+                                      (16, 1, 128), (32, 4, 96), (8, 2, 256),
+                                      (64, 4, 128)])  # the last: Qwen3-235B-A22B attention
 @pytest.mark.parametrize("Q,S", [(1, 1), (1, 300), (7, 7), (61, 1085), (130, 130)])
 def test_shapes_causal_and_masked(device, Hq, Hkv, D, Q, S):
     if D == 256 and Hq // Hkv > 4:
