@@ -154,6 +154,32 @@ class _Replay:
         return self.state
 
 
+_SLOT_FIELDS = ("slot_id", "generation", "active_leases", "last_used_sequence", "ready",
+                "pending_use_guards")
+
+
+def logical_state(snapshots) -> dict:
+    """The logical state the replay works on, read from one snapshot per
+    layer cache (in layer order): per layer its capacity, LRU and submission
+    sequences and counters, and per slot its expert id (the id within the
+    layer), generation, leases, last use, readiness and pending use guards."""
+    from dataclasses import fields
+
+    layers = []
+    for lid, snap in enumerate(snapshots):
+        slots = []
+        for s in snap.slots:
+            row = {name: getattr(s, name) for name in _SLOT_FIELDS}
+            row["expert_id"] = None if s.expert_id is None else s.expert_id.expert_id
+            slots.append(row)
+        counters = {f.name: getattr(snap.stats, f.name) for f in fields(snap.stats)}
+        layers.append({"layer_id": lid, "capacity": snap.capacity,
+                       "lru_sequence": snap.lru_sequence,
+                       "submission_sequence": snap.submission_sequence,
+                       "counters": counters, "slots": slots})
+    return {"layers": layers}
+
+
 def replay_events(pre: dict, events, actual: set, variant: str) -> dict:
     """Post-state of ``pre`` after ``events`` (CompactTransitions tuples)
     under ``variant``; ``actual`` is the set of (layer, expert) the routers

@@ -18,7 +18,13 @@ offloaded-model test compares against HF eager
   context, 12 slots per layer) and the cold 128-token forward (every cache
   emptied first): forward hooks capture every layer's router input and
   output and every MoE block's input and output; routing is checked on all
-  48 layers, the MoE output on four.
+  48 layers, the MoE output on four;
+* both 48-layer forwards again under Qwen3ExpertPrefetch, the executor the
+  reference measures its decodes in (no predictions with lookahead 0, and
+  the forward's own routes as predictions with lookahead 1): the same
+  oracle checks, plus every layer bitwise equal to the per-layer forward
+  from the same cache state; and a cold forward over four distinct coded
+  expert sets under that executor.
 
 The layer configurations run with raw transfers and with exponent-coded
 records (the benchmark default): both must meet the oracle, and give the
@@ -185,7 +191,7 @@ def _raw_and_coded(device, layer, image, where: str, **kwargs):
 def test_c2_layer_64_tokens_24_slots_zipf(device, zipf_layer, zipf_image):
     layer, experts32 = zipf_layer
     h, logits, w, idx, out, misses = _raw_and_coded(device, layer, zipf_image, "C2", tokens=64,
-                                                    slots=24, prewarm=4, seed0=1)
+                                                    slots=24, prewarm=32, seed0=1)
     print(f"C2: {misses} misses in the measured forward", flush=True)
     assert misses > 0  # the miss path (H2D + per-group launches) is exercised
     o_idx, o_w = _check_routing(h, layer.router, logits, w, idx, "C2")
@@ -278,7 +284,11 @@ def _captured_forward(loaded, cache, tree, seed_token):
     return res, gate_in, gate_out, moe_in, moe_out
 
 
-def _check_48_layers(loaded, captured, experts32, tokens: int, where: str):
+def _check_48_layers(loaded, captured, experts32, tokens: int, where: str,
+                     moe_layers=(0, 16, 32, 47)):
+    """Routing bit-exact on all 48 layers; the MoE output of ``moe_layers``
+    against the fp32 oracle.  ``experts32`` is one fp32 expert image, or a
+    function of the layer id returning that layer's image."""
     _, gate_in, gate_out, moe_in, moe_out = captured
     layers = loaded.model.model.layers
     assert len(gate_out) == len(moe_out) == 48
@@ -290,9 +300,10 @@ def _check_48_layers(loaded, captured, experts32, tokens: int, where: str):
         hid, m_idx, m_w = moe_in[lid]
         assert torch.equal(m_idx, idx) and torch.equal(m_w, w)
     errs = []
-    for lid in (0, 16, 32, 47):
+    for lid in moe_layers:
         hid, m_idx, m_w = moe_in[lid]
-        errs.append(_check_moe(hid, m_idx.cpu().numpy(), _bits(m_w), moe_out[lid], experts32,
+        image = experts32(lid) if callable(experts32) else experts32
+        errs.append(_check_moe(hid, m_idx.cpu().numpy(), _bits(m_w), moe_out[lid], image,
                                f"{where} layer {lid}", bf16_check=False))
     return errs
 
@@ -367,3 +378,153 @@ def test_c4_verify48_coded_transfers_reproduce_raw_bit_for_bit(device, verify_mo
                 assert all(torch.equal(x, y) for x, y in pairs), f"layer {lid} part {part}"
     finally:
         coded.close()
+
+
+# ------------------------------- the reference's measured decode executor --
+def _routed_sets(captured) -> dict[int, tuple[int, ...]]:
+    """Each layer's routed experts, read from the router outputs' indices."""
+    return {lid: tuple(sorted(set(out[2].flatten().tolist())))
+            for lid, out in captured[2].items()}
+
+
+def _assert_same_forward(a, b, where: str) -> None:
+    """Gate inputs/outputs and MoE inputs/outputs of every layer, bit for bit."""
+    for part, name in enumerate(("gate input", "gate output", "MoE input", "MoE output"), 1):
+        for lid in range(48):
+            x, y = a[part][lid], b[part][lid]
+            pairs = zip(x, y) if isinstance(x, tuple) else [(x, y)]
+            assert all(torch.equal(u, v) for u, v in pairs), f"{where}: layer {lid} {name}"
+
+
+def _scheduled_forward(loaded, kv, tree, seed_token, predictions, lookahead):
+    with loaded.prefetch_experts(predictions, lookahead_layers=lookahead,
+                                 max_inflight=2) as sched:
+        captured = _captured_forward(loaded, kv, tree, seed_token)
+    kv.crop(1024)
+    stats = sched.stats()
+    assert stats["complete"]
+    assert all(c.active_lease_count == 0 for c in loaded.expert_caches)
+    return captured, stats
+
+
+def _per_layer_then_scheduled(loaded, kv, tree, seed_token, executor: str):
+    """The per-layer forward and the scheduled forward of the same tree
+    from the same cache state: every cache is checkpointed (slot weights
+    and policy state), the per-layer forward runs, the checkpoints are put
+    back, then the forward runs under ``prefetch_experts`` as the
+    reference's measured decode calls it (no predictions, lookahead 0,
+    two credits) or with the forward's own routes as predictions and
+    lookahead 1."""
+    torch.cuda.synchronize()
+    marks = [c._capture_checkpoint() for c in loaded.expert_caches]
+    layer_path = _captured_forward(loaded, kv, tree, seed_token)
+    kv.crop(1024)
+    torch.cuda.synchronize()
+    for cache, mark in zip(loaded.expert_caches, marks):
+        cache._restore_checkpoint(mark)
+    del marks
+    if executor == "ready_demand":
+        predictions, lookahead = {}, 0
+    else:
+        predictions, lookahead = _routed_sets(layer_path), 1
+    scheduled, stats = _scheduled_forward(loaded, kv, tree, seed_token, predictions, lookahead)
+    return layer_path, scheduled, stats
+
+
+def _print_stats(where: str, stats: dict) -> dict:
+    rows = stats["layers"]
+    total = {k: sum(r[k] for r in rows) for k in
+             ("actual_experts", "ready_at_router", "inflight_at_router", "missing_at_router",
+              "prediction_copies", "demand_copies", "unused_prediction_copies",
+              "compute_waits")}
+    total.update(slot_wait_copies=stats["slot_wait_copies"],
+                 queue_capacity_waits=stats["queue_capacity_waits"],
+                 peak_inflight=stats["peak_inflight"])
+    print(f"{where}: {total}", flush=True)
+    return total
+
+
+@pytest.mark.parametrize("executor", ["ready_demand", "predicted"])
+@pytest.mark.parametrize("workload", ["C4", "C5"])
+def test_48_layer_forward_under_the_prefetch_scheduler(device, verify_model, workload,
+                                                       executor):
+    """C4 (60-node tree over warm caches) and C5 (128 tree tokens from empty
+    caches) under Qwen3ExpertPrefetch, the executor every measured decode of
+    the reference runs in (scripts/run_specfit_main_comparison.py:553-554):
+    routing bit-exact against the oracle on all 48 layers, MoE outputs
+    against the fp32 oracle on layers 0/16/32/47, and every layer's gate
+    and MoE inputs and outputs bitwise those of the per-layer forward from
+    the same cache state (tests/gpu/test_qwen3_expert_prefetch.py:77-100)."""
+    from specfit_amd.runtime import synthetic_tree
+
+    loaded, kv, experts32 = verify_model
+    vocab = loaded.model.config.vocab_size
+    where = f"{workload} {executor}"
+    torch.cuda.synchronize()
+    if workload == "C5":
+        loaded.cold_reset_expert_caches()
+        tree, tokens = synthetic_tree(127, 6, seed=210, vocab=vocab), 128
+    else:
+        # A different tree first, so the measured forward starts from the
+        # residency a previous verification left behind.
+        warm = synthetic_tree(60, 6, seed=111, vocab=vocab)
+        with torch.inference_mode():
+            from specfit_amd.runtime import verify_draft_tree
+            verify_draft_tree(loaded.model, warm, torch.tensor([[5]], device=device), kv,
+                              commit=False)
+        kv.crop(1024)
+        tree, tokens = synthetic_tree(60, 6, seed=110, vocab=vocab), 61
+    seed_token = torch.tensor([[31]], device=device)
+    before = [c.stats().h2d_submissions for c in loaded.expert_caches]
+    layer_path, scheduled, stats = _per_layer_then_scheduled(loaded, kv, tree, seed_token,
+                                                             executor)
+    misses = sum(c.stats().h2d_submissions for c in loaded.expert_caches) - sum(before)
+    total = _print_stats(where, stats)
+    assert misses > 0
+    assert total["actual_experts"] == sum(len(v) for v in _routed_sets(scheduled).values())
+    if executor == "predicted":
+        assert total["unused_prediction_copies"] == 0
+        assert total["prediction_copies"] > 0
+    else:
+        assert total["prediction_copies"] == 0
+    # Both credits busy with transfers while routed experts wait: the host
+    # blocks for a credit (thousands of times per forward at this size).
+    # Demand copies forced into a busy slot occur here only when the timing
+    # makes every writable slot pending (28 per C4 forward when measured);
+    # tests/test_gpu_prefetch_model.py forces that path deterministically.
+    assert total["queue_capacity_waits"] > 0
+    _assert_same_forward(layer_path, scheduled, where)
+    _check_48_layers(loaded, scheduled, experts32, tokens, where)
+
+
+def test_cold48_distinct_coded_sets_under_ready_demand(device):
+    """The bench's own 48-layer setup under the reference's executor: four
+    distinct expert sets (layer l copies from set l mod 4, raw sets in
+    pageable memory, coded records page-locked), coded transfers, empty
+    12-slot caches, 128 tree tokens.  Routing bit-exact on all layers; the
+    MoE output of one layer per set against the fp32 oracle of that set."""
+    from specfit_amd.runtime import synthetic_tree
+    from specfit_amd.workloads import make_kv_context, make_layer_sources, make_verify_model
+
+    sets = make_layer_sources(4, device=device, seed=40, pin_memory=False)
+    loaded = make_verify_model(device=device, layers=48, slots_per_layer=12,
+                               layer_sources=[sets[l % 4] for l in range(48)],
+                               compress_expert_sources=True)
+    try:
+        kv = make_kv_context(loaded.model.config, 1024, device=device, seed=2)
+        images = [_Fp32Experts(s) for s in sets]
+        tree = synthetic_tree(127, 6, seed=220, vocab=loaded.model.config.vocab_size)
+        torch.cuda.synchronize()
+        loaded.cold_reset_expert_caches()
+        before = sum(c.h2d_bytes for c in loaded.expert_caches)
+        captured, stats = _scheduled_forward(loaded, kv, tree, torch.tensor([[37]], device=device),
+                                             {}, 0)
+        moved = sum(c.h2d_bytes for c in loaded.expert_caches) - before
+        total = _print_stats("cold48 distinct coded ready_demand", stats)
+        copies = sum(c.stats().h2d_submissions for c in loaded.expert_caches)
+        assert copies >= 48 * 100 and total["demand_copies"] == copies
+        assert moved < 0.70 * copies * sets[0].shape[1] * 2  # coded records over the link
+        _check_48_layers(loaded, captured, lambda lid: images[lid % 4], 128,
+                         "cold48 distinct coded", moe_layers=(0, 17, 34, 47))
+    finally:
+        loaded.close()

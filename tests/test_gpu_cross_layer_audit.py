@@ -1,80 +1,81 @@
-"""Cross-layer prefetch audit on the device (the reference's
-tests/gpu/test_cross_layer_prefetch_audit.py restated): for each runtime
-variant -- demand, one-ahead, the ready-first scheduler without predictions,
-predicted same-layer and cross-layer, and wrong cross-layer predictions --
-from a cold and from a partly filled cache, the cache transitions the live
-caches record must replay (oracle/cache_events.py, an independent
-restatement of the reference's audit) to exactly the caches' final logical
-state: slots, generations, LRU and submission sequences and counters."""
+"""Cross-layer prefetch audit on the device.
+
+For every runtime variant (``oracle.cache_events.VARIANTS``: demand,
+one-ahead, the ready-first scheduler without predictions, predicted
+same-layer and cross-layer, wrong cross-layer predictions), slot count and
+starting state, one forward of the toy target (tests/_toy_target.py) runs
+with a compact observer on every layer cache.  The recorded transitions,
+replayed by the oracle's independent restatement of the reference's audit
+(src/specfit/cross_layer_prefetch.py:49-142) from the caches' logical state
+before the forward, must give exactly their logical state after it: slots,
+generations, LRU and submission sequences and counters.  The variants and
+the predictions they run with are the reference audit's
+(tests/gpu/test_cross_layer_prefetch_audit.py).
+"""
+from __future__ import annotations
+
 from contextlib import nullcontext
-from dataclasses import asdict
 
 import pytest
 import torch
 
-from oracle.cache_events import VARIANTS, CompactTransitions, replay_events
-from specfit_amd.runtime import ExpertKey
-from test_gpu_prefetch_model import _case, _close
+from _toy_target import ROUTES, toy_case
+from oracle.cache_events import VARIANTS, CompactTransitions, logical_state, replay_events
 
 pytestmark = pytest.mark.gpu
 
+LAYERS = 2
+ROUTED = sorted({e for row in ROUTES for e in row})  # experts 0..4; 5 is never routed
 
-def _logical(caches):
-    layers = []
-    for lid, cache in enumerate(caches):
-        snap = cache.snapshot()
-        slots = []
-        for s in snap.slots:
-            row = asdict(s)
-            row["expert_id"] = None if s.expert_id is None else s.expert_id.expert_id
-            slots.append(row)
-        layers.append(dict(layer_id=lid, capacity=snap.capacity, lru_sequence=snap.lru_sequence,
-                           submission_sequence=snap.submission_sequence,
-                           counters=asdict(snap.stats), slots=slots))
-    return dict(layers=layers)
+# variant -> (one-ahead H2D prefetch, scheduler predictions or None, lookahead)
+HOW = {
+    "demand": (False, None, 0),
+    "one_ahead": (True, None, 0),
+    "ready_demand": (False, {}, 0),
+    "predicted_same_layer": (False, dict.fromkeys(range(LAYERS), ROUTED), 0),
+    "predicted_cross_layer": (False, dict.fromkeys(range(LAYERS), ROUTED), 1),
+    "wrong_cross_layer": (False, dict.fromkeys(range(LAYERS), [5]), 1),
+}
 
 
-@pytest.mark.parametrize("slots", [2, 6])
-def test_observed_events_reconstruct_the_live_caches_for_all_variants(device, slots):
-    loaded, _, inputs = _case(slots=slots)
+def test_every_variant_has_a_way_to_run():
+    assert set(HOW) == set(VARIANTS)
+
+
+def _audited_forward(case, variant: str):
+    """(logical state before, transitions, logical state after) of one
+    forward run the way ``variant`` runs it."""
+    one_ahead, predictions, lookahead = HOW[variant]
+    before = logical_state(case.loaded.cache_snapshots())
+    recorder = CompactTransitions()
+    for cache in case.caches:
+        cache._observer = recorder
     try:
-        for variant in VARIANTS:
-            for natural in (False, True):
-                loaded.cold_reset_expert_caches()
-                if natural:
-                    for lid, cache in enumerate(loaded.expert_caches):
-                        for e in (0, 5):
-                            with cache.acquire(ExpertKey(lid, e)) as lease:
-                                lease.wait()
-                torch.cuda.synchronize()
-                pre = _logical(loaded.expert_caches)
-                observer = CompactTransitions()
-                for cache in loaded.expert_caches:
-                    cache._observer = observer
-                loaded.set_expert_h2d_prefetch(variant == "one_ahead")
-                if variant == "ready_demand":
-                    predictions = {}
-                elif variant == "wrong_cross_layer":
-                    predictions = {lid: [5] for lid in range(2)}
-                else:
-                    predictions = {lid: list(range(5)) for lid in range(2)}
-                if variant in VARIANTS[:2]:
-                    context = nullcontext()
-                else:
-                    context = loaded.prefetch_experts(
-                        predictions, lookahead_layers=int(variant in VARIANTS[4:]))
-                with torch.inference_mode(), context:
-                    loaded.model(*inputs)
-                torch.cuda.synchronize()
-                for cache in loaded.expert_caches:
-                    cache._observer = None
-                actual = {(lid, e) for lid in range(2) for e in range(5)}
-                post = _logical(loaded.expert_caches)
-                print(f"audit slots={slots} {variant} natural={natural}: "
-                      f"{len(observer.events)} transitions", flush=True)
-                assert replay_events(pre, observer.events, actual, variant) == post, \
-                    (slots, variant, natural)
+        case.loaded.set_expert_h2d_prefetch(one_ahead)
+        scheduling = (nullcontext() if predictions is None else
+                      case.loaded.prefetch_experts(predictions, lookahead_layers=lookahead))
+        with torch.inference_mode(), scheduling:
+            case.forward()
+        torch.cuda.synchronize()
     finally:
-        for cache in loaded.expert_caches:
+        for cache in case.caches:
             cache._observer = None
-        _close(loaded)
+    return before, recorder.events, logical_state(case.loaded.cache_snapshots())
+
+
+@pytest.mark.parametrize("start", ["cold", "two_resident"])
+@pytest.mark.parametrize("slots", [2, 6])
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_recorded_transitions_replay_to_the_live_caches(device, variant, slots, start):
+    case = toy_case(slots=slots, layers=LAYERS)
+    try:
+        case.loaded.cold_reset_expert_caches()
+        if start == "two_resident":
+            case.make_resident((0, 5))  # one routed expert and one never routed
+        torch.cuda.synchronize()
+        before, events, after = _audited_forward(case, variant)
+        print(f"audit {variant} slots={slots} {start}: {len(events)} transitions", flush=True)
+        routed = {(lid, e) for lid in range(LAYERS) for e in ROUTED}
+        assert replay_events(before, events, routed, variant) == after
+    finally:
+        case.close()

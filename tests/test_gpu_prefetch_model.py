@@ -13,80 +13,30 @@ import tempfile
 from contextlib import ExitStack
 from pathlib import Path
 import time
-from types import MappingProxyType, SimpleNamespace
+from types import MappingProxyType
 from unittest.mock import patch
 
 import pytest
 import torch
-from torch import nn
 
+from _toy_target import (assert_quiet, close_loaded, save_per_expert_checkpoint,
+                         tiny_qwen3_config, toy_case)
 from specfit_amd import ops
-from specfit_amd.runtime import (ExpertKey, GpuExpertCache, LoadedOffloadedQwen3,
-                                 Qwen3OffloadedExperts, RecordingCacheTransitionObserver,
-                                 RuntimeEventKind, load_offloaded_qwen3)
+from specfit_amd.runtime import ExpertKey, RuntimeEventKind, load_offloaded_qwen3
 from specfit_amd.runtime import qwen3_offloaded_experts as implementation
 
 pytestmark = pytest.mark.gpu
 
 
-class _Attention(nn.Module):
-    def forward(self, hidden):
-        return hidden.clone()
-
-
-class _Model(nn.Module):
-    def __init__(self, experts):
-        super().__init__()
-        self.model = nn.Module()
-        self.model.layers = nn.ModuleList()
-        self.config = SimpleNamespace(num_hidden_layers=len(experts))
-        for module in experts:
-            layer = nn.Module()
-            layer.self_attn = _Attention()
-            layer.mlp = nn.Module()
-            layer.mlp.experts = module
-            self.model.layers.append(layer)
-
-    def forward(self, hidden, indices, weights):
-        for layer in self.model.layers:
-            hidden = layer.self_attn(hidden)
-            hidden = layer.mlp.experts(hidden, indices, weights)
-        return hidden
-
-
 def _case(slots=3, layers=2):
-    g = torch.Generator().manual_seed(909)
-    caches, experts = [], []
-    observer = RecordingCacheTransitionObserver(run_id="predicted-prefetch")
-    for lid in range(layers):
-        sources = {ExpertKey(lid, e): torch.randn(3 * 16 * 12, generator=g, dtype=torch.bfloat16) / 16
-                   for e in range(6)}
-        cache = GpuExpertCache(sources, slot_count=slots, device="cuda:0",
-                               cache_id=f"qwen3-layer-{lid}", queue_id=f"layer-{lid}-copy",
-                               observer=observer)
-        caches.append(cache)
-        experts.append(Qwen3OffloadedExperts(layer_id=lid, cache=cache, hidden_size=16,
-                                             intermediate_size=12, h2d_prefetch=False))
-    loaded = LoadedOffloadedQwen3(_Model(experts), tuple(caches), None)
-    inputs = (torch.randn(4, 16, generator=g, dtype=torch.bfloat16).cuda(),
-              torch.tensor([[4, 0, 2], [1, 4, 3], [2, 0, 1], [4, 3, 0]], device="cuda:0"),
-              torch.rand(4, 3, generator=g, dtype=torch.bfloat16).cuda())
-    return loaded, observer, inputs
+    """(loaded model, recording observer, inputs) of a toy offloaded target
+    (tests/_toy_target.py)."""
+    case = toy_case(slots, layers)
+    return case.loaded, case.observer, case.inputs
 
 
-def _assert_restored(loaded, streams):
-    torch.cuda.synchronize()
-    for layer, cache, stream in zip(loaded.model.model.layers, loaded.expert_caches, streams):
-        assert cache.copy_stream is stream
-        assert layer.mlp.experts._prediction_scheduler is None
-        snap = cache.snapshot()
-        assert not snap.pending_transfers
-        assert all(not s.active_leases and not s.pending_use_guards for s in snap.slots)
-
-
-def _close(loaded):
-    torch.cuda.synchronize()
-    loaded.close()
+_assert_restored = assert_quiet
+_close = close_loaded
 
 
 def test_bitwise_outputs_with_correct_missing_wrong_and_duplicate_predictions(device):
@@ -258,6 +208,37 @@ def test_speculation_never_queues_a_busy_slot_wait(device):
     _close(loaded)
 
 
+def test_demand_copy_into_a_busy_slot_when_no_slot_is_writable(device):
+    """One slot, and the first expert's kernel held behind a device sleep:
+    its slot's use guard stays pending, so no slot is writable when the
+    next routed expert needs a copy, and the scheduler forces that demand
+    copy into the busy slot (the copy waits for the reader on the GPU).
+    The output is unchanged."""
+    loaded, _, inputs = _case(slots=1, layers=1)
+    expected = loaded.model(*inputs)
+    loaded.cold_reset_expert_caches()
+    real = implementation._expert_forward
+    held = []
+
+    def held_forward(*args, **kwargs):
+        if not held:
+            torch.cuda._sleep(200_000_000)  # on the stream the launch uses
+            held.append(1)
+        return real(*args, **kwargs)
+
+    streams = tuple(c.copy_stream for c in loaded.expert_caches)
+    with patch.object(implementation, "_expert_forward", held_forward):
+        with loaded.prefetch_experts({}, lookahead_layers=0) as sched:
+            actual = loaded.model(*inputs)
+    assert held
+    assert torch.equal(actual, expected)
+    _assert_restored(loaded, streams)
+    st = sched.stats()
+    print(f"forced slot-wait copies {st['slot_wait_copies']}", flush=True)
+    assert st["complete"] and st["slot_wait_copies"] >= 1
+    _close(loaded)
+
+
 def test_cross_layer_submission_is_observable(device):
     for depth in (0, 1):
         loaded, _, inputs = _case(slots=6)
@@ -400,40 +381,8 @@ def test_invalid_configuration_and_context_misuse(device):
 
 
 # ------------------------------------------------------------------ loader --
-def _tiny_config(layers=1):
-    from transformers import Qwen3MoeConfig
-    return Qwen3MoeConfig(dtype=torch.bfloat16, vocab_size=64, hidden_size=32, intermediate_size=48,
-                          moe_intermediate_size=16, num_hidden_layers=layers,
-                          num_attention_heads=4, num_key_value_heads=2, num_experts=4,
-                          num_experts_per_tok=2, max_position_embeddings=64, bos_token_id=1,
-                          eos_token_id=2, pad_token_id=0, use_cache=True)
-
-
-def _save_qwen3_style_checkpoint(model, root):
-    """Per-expert key layout of the original Qwen3 checkpoints."""
-    from safetensors.torch import save_file
-    root = Path(root)
-    model.config.save_pretrained(root)
-    out = {}
-    I = model.config.moe_intermediate_size
-    for name, tensor in model.state_dict().items():
-        if name.endswith(".experts.gate_up_proj"):
-            prefix = name[: -len("gate_up_proj")]
-            for e in range(model.config.num_experts):
-                out[f"{prefix}{e}.gate_proj.weight"] = tensor[e, :I].contiguous()
-                out[f"{prefix}{e}.up_proj.weight"] = tensor[e, I:].contiguous()
-        elif name.endswith(".experts.down_proj"):
-            prefix = name[: -len("down_proj")]
-            for e in range(model.config.num_experts):
-                out[f"{prefix}{e}.down_proj.weight"] = tensor[e].contiguous()
-        else:
-            out[name] = tensor.contiguous()
-    shard = "model-00001-of-00001.safetensors"
-    save_file(out, root / shard)
-    total = sum(t.numel() * t.element_size() for t in out.values())
-    (root / "model.safetensors.index.json").write_text(
-        json.dumps({"metadata": {"total_size": total}, "weight_map": {n: shard for n in out}}),
-        encoding="utf-8")
+_tiny_config = tiny_qwen3_config
+_save_qwen3_style_checkpoint = save_per_expert_checkpoint
 
 
 def test_loader_matches_hf_eager_and_switches_policies(device):
@@ -468,6 +417,41 @@ def test_loader_matches_hf_eager_and_switches_policies(device):
             torch.testing.assert_close(expected.float().cpu(), hf, rtol=3e-2, atol=3e-2)
         with pytest.raises(RuntimeError, match="open caches"):
             loaded.set_expert_h2d_prefetch(True)
+
+
+def test_loader_can_keep_the_eager_dense_modules(device):
+    """hip_dense_kernels=False keeps HF's RMSNorm and attention modules (for
+    equivalence checks); the default swaps them for the HIP kernels.  Both
+    models agree with HF eager within the MoE tolerance."""
+    from transformers import Qwen3MoeForCausalLM
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import (Qwen3MoeAttention,
+                                                                  Qwen3MoeRMSNorm)
+
+    from specfit_amd.runtime import Qwen3RMSNormHip
+
+    torch.manual_seed(919)
+    source = Qwen3MoeForCausalLM(_tiny_config(2)).to(torch.bfloat16)
+    source.config._experts_implementation = "eager"
+    ids = torch.tensor([[3, 9, 27, 17, 5]])
+    with torch.inference_mode():
+        hf = source(ids, use_cache=False).logits.float()
+    with tempfile.TemporaryDirectory() as root:
+        _save_qwen3_style_checkpoint(source, root)
+        with pytest.raises(ValueError, match="hip_dense_kernels"):
+            load_offloaded_qwen3(root, device=device, slots_per_layer=2, hip_dense_kernels=1)
+        for hip in (False, True):
+            with load_offloaded_qwen3(root, device=device, slots_per_layer=2,
+                                      hip_dense_kernels=hip) as loaded:
+                mods = list(loaded.model.modules())
+                eager_norms = sum(isinstance(m, Qwen3MoeRMSNorm) for m in mods)
+                hip_norms = sum(isinstance(m, Qwen3RMSNormHip) for m in mods)
+                eager_attn = sum(type(m) is Qwen3MoeAttention for m in mods)
+                # 2 layers x (input, post-attention, q, k) + the final norm
+                assert (eager_norms, hip_norms) == ((0, 9) if hip else (9, 0)), hip
+                assert eager_attn == (0 if hip else 2), hip
+                with torch.inference_mode():
+                    got = loaded.model(ids.to(device), use_cache=False).logits.float().cpu()
+                torch.testing.assert_close(got, hf, rtol=3e-2, atol=3e-2)
 
 
 def test_packed_checkpoint_loads_bitwise_equal_to_original(device):

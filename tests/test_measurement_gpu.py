@@ -1,6 +1,6 @@
 """bench.py's output contract on a GPU: one JSON line on stdout with the
-metric, whole-job value, roofline and CPU-baseline objects, run briefly
-(2 timed + 2 recorded steps) as a child process."""
+metric, whole-job value, roofline, CPU-baseline and raw-transfer objects,
+run briefly (2 timed + 2 recorded steps per pass) as a child process."""
 import json
 import os
 import subprocess
@@ -42,6 +42,12 @@ def test_bench_prints_one_contract_line(device):
     assert 0.64 * h["expert_bytes"] < h["bytes"] < 0.69 * h["expert_bytes"]
     dec = d["decode"]
     assert dec["count"] == h["transfers"] and 0 < dec["frac"] < 1
+    # the reference's raw transfers, measured beside the coded headline
+    raw = d["raw_transfer"]
+    assert raw["value"] > 0 and raw["unit"] == "tokens/s"
+    assert raw["value"] == pytest.approx(2 * 64 / (raw["ms_per_step"] * 2e-3), rel=1e-6)
+    assert raw["misses_per_step"] > 0 and raw["h2d_gbs"] > 0
+    assert 0 < raw["k3_in_step_gbs"] < 8000.0
 
 
 

@@ -81,3 +81,40 @@ def test_accurate_prediction_must_not_evict_an_unconsumed_routed_expert():
               ("evict", 0, 9, 0, 2, None, 3)]
     with pytest.raises(ValueError, match="accurate prefetch"):
         replay_events(_pre(slots=3), events, {(0, 3), (0, 5)}, "predicted_same_layer")
+
+
+def test_logical_state_reads_snapshots_into_the_replay_format():
+    """A two-slot snapshot (one slot empty, one holding expert 3 of layer 0)
+    becomes the state dict the replay consumes, and an empty snapshot is
+    exactly the hand-built pre-state above."""
+    from oracle.cache_events import logical_state
+    from specfit_amd.runtime import (CacheSlotSnapshot, ExpertCacheStats, ExpertKey,
+                                     GpuExpertCacheSnapshot)
+
+    def snap(slots, **seq):
+        return GpuExpertCacheSnapshot(
+            cache_id="qwen3-layer-0", queue_id="layer-0-copy", capacity=len(slots),
+            host_state_version=0, slots=tuple(slots), pending_transfers=(),
+            stats=ExpertCacheStats(h2d_submissions=seq.get("sub", 0), resident_hits=0,
+                                   inflight_joins=0, evictions=0, pending_use_guards=0),
+            lru_sequence=seq.get("lru", 0), submission_sequence=seq.get("sub", 0))
+
+    empty = [CacheSlotSnapshot(slot_id=s, expert_id=None, generation=0, active_leases=0,
+                               last_used_sequence=0, ready=False, pending_use_guards=0)
+             for s in range(2)]
+    assert logical_state([snap(empty)]) == _pre()
+    held = CacheSlotSnapshot(slot_id=1, expert_id=ExpertKey(0, 3), generation=1,
+                             active_leases=0, last_used_sequence=2, ready=True,
+                             pending_use_guards=0)
+    state = logical_state([snap([empty[0], held], lru=2, sub=1)])
+    layer = state["layers"][0]
+    assert layer["slots"][1] == dict(slot_id=1, expert_id=3, generation=1, active_leases=0,
+                                     last_used_sequence=2, ready=True, pending_use_guards=0)
+    assert (layer["lru_sequence"], layer["submission_sequence"]) == (2, 1)
+    assert layer["counters"]["h2d_submissions"] == 1
+    # the replay continues from it: evict 3, copy 7 into slot 1
+    events = [("evict", 0, 7, 1, 2, None, 3), ("h2d_submit", 0, 7, 1, 2, 1, None),
+              ("consume_wait", 0, 7, 1, 2, None, None), ("release", 0, 7, 1, 2, None, None)]
+    post = replay_events(state, events, {(0, 7)}, "demand")
+    assert post["layers"][0]["slots"][1]["expert_id"] == 7
+    assert post["layers"][0]["counters"]["evictions"] == 1
