@@ -98,6 +98,9 @@ def parse_args():
     p.add_argument("--max-inflight", type=int, default=2,
                    help="the scheduler's bound on incomplete transfers (default 2, the "
                         "reference's default)")
+    p.add_argument("--no-raw-pass", dest="raw_pass", action="store_false",
+                   help="single-layer workload with coded transfers: skip the second pass with "
+                        "raw transfers (reported as raw_transfer)")
     p.add_argument("--record", choices=("full", "k3", "none"), default="full",
                    help="timing events of the recorded pass: K3 launches + one copy window "
                         "per step (full), K3 only, or none (no recorded pass)")
@@ -417,6 +420,7 @@ def main_verify(args) -> int:
             "complete": all(st["complete"] for st in timed),
             "peak_inflight": max(st["peak_inflight"] for st in timed),
             "queue_capacity_waits": sum(st["queue_capacity_waits"] for st in timed) / len(timed),
+            "slot_wait_copies": sum(st["slot_wait_copies"] for st in timed) / len(timed),
             "per_forward": {k: sum(r[k] for r in rows) / len(timed)
                             for k in ("predicted_experts", "actual_experts", "ready_at_router",
                                       "inflight_at_router", "missing_at_router",
@@ -571,60 +575,25 @@ def main() -> int:
         return main_workload(args)
 
 
-def main_workload(args) -> int:
-    """Run the workload ``args`` names and print its JSON line."""
-    if args.workload in ("verify48", "cold48"):
-        if args.workload == "cold48" and args.tree_nodes == 60:
-            args.tree_nodes = 127  # 128 tree tokens
-        return main_verify(args)
-    if args.workload == "sweep":
-        return main_sweep(args)
-    if args.workload == "resident16":
-        args.tokens, args.slots = 16, 128
-
+def _layer_pass(args, dev, layer, router, hidden, image, *, resident: bool) -> dict:
+    """One measurement of the single-layer workload on a fresh cache:
+    pre-warm (``args.prewarm`` cycles), warm-up, a timed pass of
+    ``args.steps`` steps without timing events, then (unless ``--record
+    none``) a recorded pass over the next inputs with HIP events around
+    every K3 launch and copy window.  ``image`` selects coded transfers
+    (None: raw bytes)."""
     import torch
 
     from specfit_amd import ops
-    from specfit_amd.codec import CompressedExperts
-    from specfit_amd.runtime import (ExpertKey, GpuExpertCache, Qwen3MoeTopKRouterHip,
-                                     Qwen3OffloadedExperts)
-    from specfit_amd.workloads import make_hidden, make_layer
+    from specfit_amd.runtime import ExpertKey, GpuExpertCache, Qwen3OffloadedExperts
 
-    if not torch.cuda.is_available():
-        print("bench.py needs a HIP device", file=sys.stderr)
-        return 1
-    dev = torch.device("cuda:0")
-    T, slots = args.tokens, args.slots
-    resident = args.workload == "resident16"
-    t0 = time.perf_counter()
-    layer = make_layer(seed=0, zipf_s=None if resident else 1.1, zipf_lambda=1.0,
-                       pin_memory=True)
-    H, I, E, K = layer.hidden_size, layer.intermediate_size, layer.num_experts, layer.top_k
-    expert_bytes = layer.expert_bytes
-    log(f"layer generated in {time.perf_counter() - t0:.1f}s "
-        f"({E} experts x {expert_bytes} B pinned)")
-
-    router = Qwen3MoeTopKRouterHip(num_experts=E, hidden_size=H, top_k=K, norm_topk_prob=True,
-                                   device=dev)
-    with torch.no_grad():
-        router.weight.copy_(layer.router)
-    image = None
-    if args.transfer == "coded":
-        t1 = time.perf_counter()
-        image = CompressedExperts.encode({ExpertKey(0, e): layer.experts[e] for e in range(E)},
-                                         device=dev)
-        log(f"experts coded in {time.perf_counter() - t1:.1f}s: {image.transfer_bytes} of "
-            f"{image.raw_bytes} B ({image.transfer_bytes / image.raw_bytes:.4f})")
-    cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(E)}, slot_count=slots,
-                           device=dev, adopt_pinned_sources=True, cache_id="qwen3-layer-0",
-                           queue_id="layer-0-copy", compressed_sources=image)
+    H, I, E = layer.hidden_size, layer.intermediate_size, layer.num_experts
+    cache = GpuExpertCache({ExpertKey(0, e): layer.experts[e] for e in range(E)},
+                           slot_count=args.slots, device=dev, adopt_pinned_sources=True,
+                           cache_id="qwen3-layer-0", queue_id="layer-0-copy",
+                           compressed_sources=image)
     experts = Qwen3OffloadedExperts(layer_id=0, cache=cache, hidden_size=H, intermediate_size=I,
                                     execution_policy="resident_first", h2d_prefetch=True)
-
-    n_inputs = args.prewarm + args.warmup + args.steps * (1 if args.record == "none" else 2)
-    hidden = [make_hidden(T, H, seed=(0 if resident else 1) + i, zipf_fold=not resident).to(dev)
-              for i in range(n_inputs)]
-    torch.cuda.synchronize()
 
     def step(h):
         _, w, idx = router(h)
@@ -634,11 +603,12 @@ def main_workload(args) -> int:
         for e in range(E):
             with cache.acquire(ExpertKey(0, e)) as lease:
                 lease.wait()
-    # Pre-warm the cache with 32 prior cycles, then untimed warm-up steps.
+    # Pre-warm the cache with the prior cycles, then untimed warm-up steps.
     for i in range(args.prewarm):
         step(hidden[i])
     torch.cuda.synchronize()
-    log(f"prewarmed {args.prewarm} cycles; cache stats {cache.stats()}")
+    log(f"prewarmed {args.prewarm} cycles ({'coded' if image is not None else 'raw'}); "
+        f"cache stats {cache.stats()}")
     for i in range(args.warmup):
         step(hidden[args.prewarm + i])
     torch.cuda.synchronize()
@@ -681,21 +651,18 @@ def main_workload(args) -> int:
         with ops.record_launches(copies=args.record == "full", park_cycles=PARK_CYCLES) as rec:
             rec_wall, rec_misses, _ = run_steps(hidden[base + args.steps:], rec)
         log(f"recorded {args.steps} steps in {rec_wall * 1e3:.2f} ms: {rec_misses} misses")
+    torch.cuda.synchronize()
+    cache.close()
+    return dict(timed=timed, wall=wall, misses=misses, hits=hits, rec=rec, rec_wall=rec_wall,
+                rec_misses=rec_misses, step_events=step_events)
 
-    # K3 (grouped SwiGLU gate/up + down dispatches) over the timed region.
+
+def _pass_figures(p: dict, k3_bytes, expert_bytes: int) -> dict:
+    """K3, H2D and overlap figures of a recorded pass from ``_layer_pass``."""
+    rec = p["rec"]
+    # K3 (grouped SwiGLU gate/up + down dispatches) over the recorded pass.
     k3 = [(n, rows, tag, s.elapsed_time(e) * 1e-3) for n, rows, tag, s, e in rec.k3]
-    k3_time = sum(x[3] for x in k3)
-
-    def k3_bytes(n, rows):
-        # expert weights + gathered hidden rows read + weighted rows written
-        return n * expert_bytes + rows * H * 2 * 2
-
-    k3_alg = sum(k3_bytes(n, r) for n, r, _, _ in k3)
     res = [x for x in k3 if x[2] == "resident"]
-    res_bytes = sum(k3_bytes(n, r) for n, r, _, _ in res)
-    res_time = sum(x[3] for x in res)
-    h2d_bytes = rec.h2d_bytes  # bytes over the link (coded records or raw experts)
-    h2d_expert_bytes = rec_misses * expert_bytes
     h2d_time = rec.copy_busy_seconds() if rec.windows else 0.0
     # Overlap of transfers and expert GEMMs: (t_h2d + t_gemm - t_union) /
     # min(t_h2d, t_gemm), with t_union the measured union of the copy windows
@@ -709,6 +676,102 @@ def main_workload(args) -> int:
         t_gemm = _union_length(spans_k3) * 1e-3
         t_h2d = _union_length(spans_copy) * 1e-3
         overlap = max(0.0, min(1.0, (t_h2d + t_gemm - t_union) / min(t_h2d, t_gemm)))
+    return dict(k3=k3, k3_time=sum(x[3] for x in k3),
+                k3_alg=sum(k3_bytes(n, r) for n, r, _, _ in k3), res=res,
+                res_bytes=sum(k3_bytes(n, r) for n, r, _, _ in res),
+                res_time=sum(x[3] for x in res),
+                h2d_bytes=rec.h2d_bytes,  # over the link (coded records or raw experts)
+                h2d_expert_bytes=p["rec_misses"] * expert_bytes, h2d_time=h2d_time,
+                overlap=overlap)
+
+
+def main_workload(args) -> int:
+    """Run the workload ``args`` names and print its JSON line."""
+    if args.workload in ("verify48", "cold48"):
+        if args.workload == "cold48" and args.tree_nodes == 60:
+            args.tree_nodes = 127  # 128 tree tokens
+        return main_verify(args)
+    if args.workload == "sweep":
+        return main_sweep(args)
+    if args.workload == "resident16":
+        args.tokens, args.slots = 16, 128
+
+    import torch
+
+    from specfit_amd import ops
+    from specfit_amd.codec import CompressedExperts
+    from specfit_amd.runtime import ExpertKey, Qwen3MoeTopKRouterHip
+    from specfit_amd.workloads import make_hidden, make_layer
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    T, slots = args.tokens, args.slots
+    resident = args.workload == "resident16"
+    t0 = time.perf_counter()
+    layer = make_layer(seed=0, zipf_s=None if resident else 1.1, zipf_lambda=1.0,
+                       pin_memory=True)
+    H, I, E, K = layer.hidden_size, layer.intermediate_size, layer.num_experts, layer.top_k
+    expert_bytes = layer.expert_bytes
+    log(f"layer generated in {time.perf_counter() - t0:.1f}s "
+        f"({E} experts x {expert_bytes} B pinned)")
+
+    router = Qwen3MoeTopKRouterHip(num_experts=E, hidden_size=H, top_k=K, norm_topk_prob=True,
+                                   device=dev)
+    with torch.no_grad():
+        router.weight.copy_(layer.router)
+    image = None
+    if args.transfer == "coded":
+        t1 = time.perf_counter()
+        image = CompressedExperts.encode({ExpertKey(0, e): layer.experts[e] for e in range(E)},
+                                         device=dev)
+        log(f"experts coded in {time.perf_counter() - t1:.1f}s: {image.transfer_bytes} of "
+            f"{image.raw_bytes} B ({image.transfer_bytes / image.raw_bytes:.4f})")
+    n_inputs = args.prewarm + args.warmup + args.steps * (1 if args.record == "none" else 2)
+    hidden = [make_hidden(T, H, seed=(0 if resident else 1) + i, zipf_fold=not resident).to(dev)
+              for i in range(n_inputs)]
+    torch.cuda.synchronize()
+
+    def k3_bytes(n, rows):
+        # expert weights + gathered hidden rows read + weighted rows written
+        return n * expert_bytes + rows * H * 2 * 2
+
+    p = _layer_pass(args, dev, layer, router, hidden, image, resident=resident)
+    rec, timed = p["rec"], p["timed"]
+    wall, misses, hits = p["wall"], p["misses"], p["hits"]
+    f = _pass_figures(p, k3_bytes, expert_bytes)
+    k3, k3_alg, k3_time = f["k3"], f["k3_alg"], f["k3_time"]
+    res_bytes, res_time, res = f["res_bytes"], f["res_time"], f["res"]
+    h2d_bytes, h2d_expert_bytes, h2d_time = f["h2d_bytes"], f["h2d_expert_bytes"], f["h2d_time"]
+    rec_wall, rec_misses, overlap = p["rec_wall"], p["rec_misses"], f["overlap"]
+    step_events = p["step_events"]
+
+    # The reference's transfer semantics beside the coded headline: a fresh
+    # cache whose misses move the raw bf16 expert bytes, the same pre-warm
+    # and the same inputs.
+    raw_pass = None
+    if image is not None and not resident and args.raw_pass:
+        q = _layer_pass(args, dev, layer, router, hidden, None, resident=False)
+        g = _pass_figures(q, k3_bytes, expert_bytes)
+        raw_pass = {
+            "value": args.steps * T / q["wall"], "unit": "tokens/s",
+            "ms_per_step": q["wall"] / args.steps * 1e3,
+            "misses_per_step": q["misses"] / args.steps,
+            "hits_per_step": q["hits"] / args.steps,
+            "h2d_gbs": g["h2d_bytes"] / g["h2d_time"] / 1e9 if g["h2d_time"] else None,
+            "h2d_link_busy_frac": g["h2d_time"] / q["rec_wall"] if g["h2d_time"] else None,
+            "overlap": g["overlap"],
+            "k3_in_step_gbs": g["k3_alg"] / g["k3_time"] / 1e9 if g["k3_time"] else None,
+            "k3_in_step_frac": (g["k3_alg"] / g["k3_time"] / 1e9 / HBM_PEAK_GBS
+                                if g["k3_time"] else None),
+            "k3_resident_in_step_gbs": (g["res_bytes"] / g["res_time"] / 1e9
+                                        if g["res_time"] else None),
+            "note": ("same workload, inputs and pre-warm with a fresh cache whose misses copy "
+                     "the raw bf16 expert bytes (9,437,184 B each), as the reference does"),
+        }
+        log(f"raw-transfer pass: {raw_pass['value']:.0f} tokens/s, "
+            f"{raw_pass['ms_per_step']:.3f} ms/step")
 
     # A plain elementwise kernel of known size (256 MiB read + 256 MiB
     # written).  Under rocprofv3 --pmc it calibrates FETCH_SIZE / WRITE_SIZE
@@ -827,8 +890,9 @@ def main_workload(args) -> int:
                             "gbs": res_launch_bytes / res_launch / 1e9,
                             "frac": res_launch_bytes / res_launch / 1e9 / HBM_PEAK_GBS},
     }
+    if raw_pass is not None:
+        line["raw_transfer"] = raw_pass
     print(json.dumps(line), flush=True)
-    cache.close()
     return 0
 
 

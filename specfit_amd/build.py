@@ -9,6 +9,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT_DIR = os.path.dirname(PKG_DIR)
@@ -16,6 +17,7 @@ CSRC_DIR = os.path.join(PKG_DIR, "csrc")
 INCLUDE_DIR = os.path.join(ROOT_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libspecfit_amd.so")
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
 OFFLOAD_ARCH = "gfx950"
 
 SOURCES = ("abi.hip", "router.hip", "dispatch.hip", "swiglu.hip", "combine.hip",
@@ -26,7 +28,6 @@ HIPCC_FLAGS = (
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # The router's bit-exact contract relies on no implicit contraction; all
     # intended fused multiply-adds are written explicitly.
     "-ffp-contract=off",
@@ -42,19 +43,34 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into LIB_PATH (always recompiles)."""
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}",
-           *(os.path.join(CSRC_DIR, s) for s in SOURCES), "-o", tmp]
+def _run(cmd: list[str]) -> str:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+        raise RuntimeError(f"hipcc failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source into LIB_PATH (always recompiles): one hipcc
+    process per source file in parallel, then one link."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    cc = hipcc()
+    objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    cmds = [[cc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-c", os.path.join(CSRC_DIR, s), "-o", o]
+            for s, o in zip(SOURCES, objs)]
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as pool:
+        errs = list(pool.map(_run, cmds))
+    tmp = LIB_PATH + ".tmp"
+    errs.append(_run([cc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *objs,
+                      "-o", tmp]))
+    if verbose:
+        for err in errs:
+            if err.strip():
+                print(err, file=sys.stderr)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -6,7 +6,10 @@ host memory into an HBM slot (gpu_expert_cache.py:556-561 of the reference
 copies the raw bf16 bytes).  A bf16 weight is sign | 8-bit exponent | 7-bit
 mantissa.  Sign and mantissa bits of weights are close to uniform; the
 exponents are not (N(0, 0.02) values put 73% of their mass in 3 binades and
-98% in 7; their entropy is 2.55 bits), and trained checkpoints look alike.
+98% in 7; their entropy is 2.55 bits).  The byte ratio below was measured
+on such synthetic weights only; no trained checkpoint is available here, so
+the ratio on real weights is not pinned.  The format is lossless for any
+weights: exponents outside an expert's tables take the raw escape.
 A record keeps, per value, one byte of sign and mantissa and a cascade of
 short exponent codes, each level a fixed-width code into a small table of
 the expert's own, its last code deferring to the next level:

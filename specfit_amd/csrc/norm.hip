@@ -39,12 +39,13 @@ __device__ __forceinline__ void unpack(uint4 v, float (&f)[8]) {
 }
 
 // VEC: rows are 16-byte aligned and dim % 8 == 0 (8-element chunks);
-// otherwise one element per lane step.
+// otherwise one element per lane step.  x and out may be the same rows (an
+// in-place call), so neither is declared __restrict__.
 template <bool VEC>
-__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const uint16_t* x,
                                                             int64_t row_stride, int rows, int dim,
                                                             const uint16_t* __restrict__ weight,
-                                                            float eps, uint16_t* __restrict__ out,
+                                                            float eps, uint16_t* out,
                                                             int64_t out_stride) {
   const int lane = threadIdx.x & (SF_WAVE - 1);
   const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / SF_WAVE;

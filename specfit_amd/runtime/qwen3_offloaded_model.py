@@ -218,7 +218,8 @@ def _pack_layer_experts(get, names: dict, E: int, H: int, I: int) -> torch.Tenso
 
 def _install(model, *, layer_packed: dict[int, torch.Tensor], device: torch.device,
              slots_per_layer: int, reduction_mode, expert_execution_policy,
-             h2d_prefetch: bool, cache_observer, compress_expert_sources: bool = False) -> tuple:
+             h2d_prefetch: bool, cache_observer, compress_expert_sources: bool = False,
+             hip_dense_kernels: bool = True) -> tuple:
     config = model.config
     caches = []
     # One pair of SDMA streams for every layer cache (layers copy in turn).
@@ -248,9 +249,11 @@ def _install(model, *, layer_packed: dict[int, torch.Tensor], device: torch.devi
                 execution_policy=expert_execution_policy, h2d_prefetch=h2d_prefetch)
             layer.mlp.gate = Qwen3MoeTopKRouterHip.from_module(layer.mlp.gate)
         # The dense layers' RMSNorms run as one kernel each (K6), and each
-        # attention layer's query/key norms and rotary embedding as one (K7).
-        install_hip_norms(model)
-        install_hip_attention(model)
+        # attention layer's query/key norms and rotary embedding as one (K7);
+        # without hip_dense_kernels they stay HF's eager modules.
+        if hip_dense_kernels:
+            install_hip_norms(model)
+            install_hip_attention(model)
     except BaseException:
         for cache in reversed(caches):
             cache.close()
@@ -267,7 +270,8 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
                          attn_implementation: str = "sdpa",
                          cache_observer: CacheTransitionObserver | None = None,
                          h2d_prefetch: bool = True,
-                         compress_expert_sources: bool = False) -> LoadedOffloadedQwen3:
+                         compress_expert_sources: bool = False,
+                         hip_dense_kernels: bool = True) -> LoadedOffloadedQwen3:
     """Load a Qwen3-MoE checkpoint with offloaded experts
     (qwen3_offloaded_model.py:667-840).  ``model_root`` holds config.json
     and the original safetensors (per-expert or fused expert tensors); with
@@ -276,7 +280,11 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
     config/index hashes (the weight shards need not exist).
     ``compress_expert_sources`` (an extension beyond the reference): every layer's
     misses move exponent-coded records (specfit_amd.codec) over the host
-    link and are decoded into the slots, which hold the same bytes."""
+    link and are decoded into the slots, which hold the same bytes.
+    ``hip_dense_kernels`` (default True): the dense layers' RMSNorms and the
+    attention layers' query/key norms and rotary embedding run as HIP
+    kernels, which may differ from HF eager by a last-place rounding of the
+    variance; False keeps HF's eager modules (for equivalence checks)."""
     from accelerate import init_empty_weights
     from safetensors import safe_open
     from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
@@ -287,6 +295,8 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
     t = {}
     if type(h2d_prefetch) is not bool:
         raise ValueError("h2d_prefetch must be a boolean")
+    if type(hip_dense_kernels) is not bool:
+        raise ValueError("hip_dense_kernels must be a boolean")
     policy = ExpertExecutionPolicy(expert_execution_policy)
     device = torch.device(device)
     if device.type != "cuda":
@@ -391,7 +401,8 @@ def load_offloaded_qwen3(model_root, *, device, slots_per_layer: int,
                       slots_per_layer=slots_per_layer, reduction_mode=reduction_mode,
                       expert_execution_policy=policy, h2d_prefetch=h2d_prefetch,
                       cache_observer=cache_observer,
-                      compress_expert_sources=compress_expert_sources)
+                      compress_expert_sources=compress_expert_sources,
+                      hip_dense_kernels=hip_dense_kernels)
     t["expert_cache_initialization_seconds"] = time.perf_counter() - t5
     t6 = time.perf_counter()
     meta = [n for n, p in model.named_parameters() if p.is_meta]
@@ -417,13 +428,17 @@ def build_offloaded_qwen3(model, *, device, slots_per_layer: int,
                           cache_observer: CacheTransitionObserver | None = None,
                           h2d_prefetch: bool = True,
                           layer_experts: dict[int, torch.Tensor] | None = None,
-                          compress_expert_sources: bool = False
+                          compress_expert_sources: bool = False,
+                          hip_dense_kernels: bool = True
                           ) -> LoadedOffloadedQwen3:
     """Offload the experts of an in-memory HF ``Qwen3MoeForCausalLM``.
 
     The model's non-expert parameters move to ``device``; its fused expert
     parameters are packed into pinned memory (or ``layer_experts[l]``, a
-    pinned ``[E, 3*I*H]`` bf16 tensor per layer, is used directly)."""
+    pinned ``[E, 3*I*H]`` bf16 tensor per layer, is used directly).
+    ``hip_dense_kernels`` as for ``load_offloaded_qwen3``."""
+    if type(hip_dense_kernels) is not bool:
+        raise ValueError("hip_dense_kernels must be a boolean")
     device = torch.device(device)
     if device.index is None:
         device = torch.device("cuda", torch.cuda.current_device())
@@ -446,7 +461,8 @@ def build_offloaded_qwen3(model, *, device, slots_per_layer: int,
                       reduction_mode=reduction_mode,
                       expert_execution_policy=ExpertExecutionPolicy(expert_execution_policy),
                       h2d_prefetch=h2d_prefetch, cache_observer=cache_observer,
-                      compress_expert_sources=compress_expert_sources)
+                      compress_expert_sources=compress_expert_sources,
+                      hip_dense_kernels=hip_dense_kernels)
     model.requires_grad_(False)
     model.eval()
     return LoadedOffloadedQwen3(model=model, expert_caches=caches, load_timings=None)
