@@ -26,6 +26,14 @@ included; median and 10th/90th percentile in `device_ms_per_step`).
 --record none skips it.  Steps per pass default to 50 (10 for the 48-layer
 forwards).
 
+The default single-layer run also reports, in the same line: a second
+measurement of the same workload whose misses copy the raw bf16 expert bytes
+as the reference does (``raw_transfer``), and shorter runs of the other
+benchmark configurations (``other_configs``: 16 tokens all resident, the
+1-128 token sweep, the 48-layer verification forward and the cold 128-token
+forward), each exactly as its ``--workload`` run measures it, with fewer
+steps.
+
 Prints ONE JSON line on stdout; diagnostics go to stderr.
 """
 from __future__ import annotations
@@ -48,7 +56,7 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def parse_args():
+def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None,
@@ -101,10 +109,15 @@ def parse_args():
     p.add_argument("--no-raw-pass", dest="raw_pass", action="store_false",
                    help="single-layer workload with coded transfers: skip the second pass with "
                         "raw transfers (reported as raw_transfer)")
+    p.add_argument("--no-other-configs", dest="other_configs", action="store_false",
+                   help="single-layer workload: skip the shorter runs of the other "
+                        "configurations (other_configs: resident16, sweep, verify48, cold48)")
+    p.add_argument("--config-steps", type=int, default=20,
+                   help="steps per pass of the resident16 and sweep runs in other_configs")
     p.add_argument("--record", choices=("full", "k3", "none"), default="full",
                    help="timing events of the recorded pass: K3 launches + one copy window "
                         "per step (full), K3 only, or none (no recorded pass)")
-    args = p.parse_args()
+    args = p.parse_args(argv)
     if args.executor != "layer" and args.workload not in ("verify48", "cold48"):
         p.error("--executor applies to the 48-layer forwards (verify48, cold48)")
     if args.lookahead is None:
@@ -228,7 +241,7 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def main_verify(args) -> int:
+def main_verify(args) -> dict:
     """The 48-layer verification forward: per step, one target forward of
     [seed, 60 draft nodes] with the tree mask against a 1024-token context
     (then the context is cropped back), every MoE block offloaded with a
@@ -426,12 +439,11 @@ def main_verify(args) -> int:
                                       "inflight_at_router", "missing_at_router",
                                       "prediction_copies", "demand_copies",
                                       "unused_prediction_copies", "compute_waits")}}
-    print(json.dumps(line), flush=True)
     loaded.close()
-    return 0
+    return line
 
 
-def main_sweep(args) -> int:
+def main_sweep(args) -> dict:
     """Tree-size sweep: 1, 8, 32, 64 and 128 tokens through one Zipf-routed
     MoE layer with a 12-slot cache (the 32 pre-warm and the warm-up inputs
     cycled for at least 0.25 s before each point's timed pass)."""
@@ -555,8 +567,7 @@ def main_sweep(args) -> int:
                        "cache_slots": slots, "prewarm_cycles": args.prewarm,
                        "transfer": args.transfer},
             "points": points}
-    print(json.dumps(line), flush=True)
-    return 0
+    return line
 
 
 def main() -> int:
@@ -572,7 +583,73 @@ def main() -> int:
     # mode, as the reference's measured decode loop does
     # (scripts/run_specfit_main_comparison.py:713).
     with torch.inference_mode():
-        return main_workload(args)
+        line = main_workload(args)
+        if args.workload == "layer" and args.other_configs:
+            line["other_configs"] = other_configs(args)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _config_run(argv: list[str], pick) -> dict:
+    """One more workload in this process (its own inputs, cache and model,
+    freed afterwards); ``pick`` keeps the figures the summary reports.  A
+    failure is reported in the summary instead of ending the run."""
+    import gc
+
+    import torch
+
+    log(f"other configuration: {' '.join(argv)}")
+    try:
+        out = pick(main_workload(parse_args(argv)))
+    except Exception as exc:  # noqa: BLE001 - reported, not raised
+        out = {"error": f"{type(exc).__name__}: {exc}"}
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    out["command"] = "python bench.py " + " ".join(argv)
+    return out
+
+
+def other_configs(args) -> dict:
+    """The other benchmark configurations, each in a shorter run of its own
+    (fewer steps; the same code path as ``--workload``):
+    16 tokens all resident; the 1-128 token sweep; the 48-layer
+    verification forward and the cold 128-token forward."""
+    steps, tr = str(args.config_steps), ["--transfer", args.transfer]
+    # The 48-layer runs take the forward's shape options of this run.
+    shape = ["--layers", str(args.layers), "--context", str(args.context),
+             "--verify-slots", str(args.verify_slots), "--expert-sets", str(args.expert_sets)]
+
+    def layer_pick(d):
+        return {"value": d["value"], "unit": d["unit"], "ms_per_step": d["ms_per_step"],
+                "workload": d["config"]["workload"], "k3_frac": d["roofline"]["frac"],
+                "k3_gbs": d["roofline"]["achieved"],
+                "cpu_baseline": d["cpu_baseline"] and {k: d["cpu_baseline"][k]
+                                                       for k in ("value", "unit", "cores")}}
+
+    def sweep_pick(d):
+        keep = ("tokens", "tokens_per_s", "ms_per_step", "misses_per_step", "k3_gbs",
+                "h2d_expert_gbs", "h2d_link_busy_frac")
+        return {"workload": d["config"]["workload"], "transfer": d["config"]["transfer"],
+                "points": [{k: p[k] for k in keep} for p in d["points"]]}
+
+    def verify_pick(d):
+        return {"value": d["value"], "unit": d["unit"], "ms_per_step": d["ms_per_step"],
+                "workload": d["config"]["workload"], "transfer": d["config"]["transfer"],
+                "per_layer_tokens_per_s": d["per_layer_tokens_per_s"],
+                "misses_per_layer": d["cache"]["misses_per_layer"]}
+
+    return {
+        "resident16": _config_run(["--workload", "resident16", "--steps", steps, "--warmup", "5",
+                                   "--cpu-seconds", "2", "--record", "k3"], layer_pick),
+        "sweep": _config_run(["--workload", "sweep", "--steps", steps, "--warmup", "5",
+                              "--record", "k3", *tr], sweep_pick),
+        "verify48": _config_run(["--workload", "verify48", "--steps", "5", "--warmup", "2",
+                                 "--record", "none", "--tree-nodes", str(args.tree_nodes),
+                                 *shape, *tr], verify_pick),
+        "cold48": _config_run(["--workload", "cold48", "--steps", "5", "--warmup", "2",
+                               "--record", "none", *shape, *tr], verify_pick),
+    }
 
 
 def _layer_pass(args, dev, layer, router, hidden, image, *, resident: bool) -> dict:
@@ -676,7 +753,24 @@ def _pass_figures(p: dict, k3_bytes, expert_bytes: int) -> dict:
         t_gemm = _union_length(spans_k3) * 1e-3
         t_h2d = _union_length(spans_copy) * 1e-3
         overlap = max(0.0, min(1.0, (t_h2d + t_gemm - t_union) / min(t_h2d, t_gemm)))
-    return dict(k3=k3, k3_time=sum(x[3] for x in k3),
+    # K3 launches that ran beside a decode (their event intervals intersect
+    # one of the recorded decodes') against those that ran alone.
+    beside = None
+    if rec.k3 and rec.decodes:
+        origin = rec.k3[0][3]
+        spans_dec = sorted((origin.elapsed_time(a), origin.elapsed_time(b))
+                           for *_, a, b in rec.decodes)
+        groups = {"beside_decode": [0, 0, 0.0], "alone": [0, 0, 0.0]}
+        for (n, rows, _, sec), (*_, a, b) in zip(k3, rec.k3):
+            s0, s1 = origin.elapsed_time(a), origin.elapsed_time(b)
+            hit = any(d0 < s1 and d1 > s0 for d0, d1 in spans_dec)
+            g = groups["beside_decode" if hit else "alone"]
+            g[0] += 1
+            g[1] += k3_bytes(n, rows)
+            g[2] += sec
+        beside = {k: {"launches": v[0], "gbs": v[1] / v[2] / 1e9 if v[2] else None}
+                  for k, v in groups.items()}
+    return dict(k3=k3, k3_time=sum(x[3] for x in k3), k3_beside_decode=beside,
                 k3_alg=sum(k3_bytes(n, r) for n, r, _, _ in k3), res=res,
                 res_bytes=sum(k3_bytes(n, r) for n, r, _, _ in res),
                 res_time=sum(x[3] for x in res),
@@ -685,8 +779,8 @@ def _pass_figures(p: dict, k3_bytes, expert_bytes: int) -> dict:
                 overlap=overlap)
 
 
-def main_workload(args) -> int:
-    """Run the workload ``args`` names and print its JSON line."""
+def main_workload(args) -> dict:
+    """Run the workload ``args`` names and return its JSON line."""
     if args.workload in ("verify48", "cold48"):
         if args.workload == "cold48" and args.tree_nodes == 60:
             args.tree_nodes = 127  # 128 tree tokens
@@ -704,8 +798,7 @@ def main_workload(args) -> int:
     from specfit_amd.workloads import make_hidden, make_layer
 
     if not torch.cuda.is_available():
-        print("bench.py needs a HIP device", file=sys.stderr)
-        return 1
+        raise SystemExit("bench.py needs a HIP device")
     dev = torch.device("cuda:0")
     T, slots = args.tokens, args.slots
     resident = args.workload == "resident16"
@@ -886,14 +979,14 @@ def main_workload(args) -> int:
         "decode": decode_stats(rec),
         "k3_resident_in_step": {"launches": len(res),
                                 "gbs": res_bytes / res_time / 1e9 if res_time else None},
+        "k3_in_step_by_decode_overlap": f["k3_beside_decode"],
         "k3_all_resident": {"experts": len(active), "rows": rows_n, "us": res_launch * 1e6,
                             "gbs": res_launch_bytes / res_launch / 1e9,
                             "frac": res_launch_bytes / res_launch / 1e9 / HBM_PEAK_GBS},
     }
     if raw_pass is not None:
         line["raw_transfer"] = raw_pass
-    print(json.dumps(line), flush=True)
-    return 0
+    return line
 
 
 if __name__ == "__main__":

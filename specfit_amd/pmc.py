@@ -30,6 +30,7 @@ CALIBRATION_BYTES = 256 << 20   # read and written by the calibration kernel
 CALIBRATION_TAG = "neg"         # substring of the calibration kernel's name
 HIDDEN, INTERMEDIATE = 2048, 768
 THREADS = 256
+DECODE_CHUNK = 4096             # values per decode workgroup (SF_DECODE_CHUNK)
 
 
 def _rows(run_dir: str) -> list[dict]:
@@ -141,6 +142,21 @@ def summarize(fetch_dir: str, write_dir: str, command: str | None = None) -> str
             lines.append(f"| {label} | {pairs} | {key} | {n} | {fb / n / 1e6:.2f} | "
                          f"{wb / n / 1e6:.3f} | {ab / n / 1e6:.2f} | {fb / ab:.3f} |")
         ratios[label] = ((fetch + write) / alg, fetch / pairs, write / pairs, alg / pairs)
+    # Coded-transfer decodes (sf_expert_decode) before the calibration kernel.
+    f_cal = [i for i, d in enumerate(f_disp) if CALIBRATION_TAG in d[1]][0]
+    w_cal = [i for i, d in enumerate(w_disp) if CALIBRATION_TAG in d[1]][0]
+    f_dec = [d for d in f_disp[:f_cal] if "decode_kernel" in d[1]]
+    w_dec = [d for d in w_disp[:w_cal] if "decode_kernel" in d[1]]
+    if f_dec and len(f_dec) == len(w_dec):
+        fetch = sum(d[3] for d in f_dec) * 1024 * f_scale / len(f_dec)
+        write = sum(d[3] for d in w_dec) * 1024 * w_scale / len(w_dec)
+        values = f_dec[0][2] // THREADS * DECODE_CHUNK  # one workgroup per chunk
+        lines += ["", "## Decodes of coded records (`decode_kernel`, scaled bytes per dispatch)", "",
+                  "| dispatches | fetch MB | write MB | values written (bf16 MB) | "
+                  "write / values |", "|---|---|---|---|---|",
+                  f"| {len(f_dec)} | {fetch / 1e6:.3f} | {write / 1e6:.3f} | "
+                  f"{2 * values / 1e6:.3f} | {write / (2 * values):.3f} |", "",
+                  f"decode_fetch_bytes: {fetch:.0f}", f"decode_write_bytes: {write:.0f}"]
     lines.append("")
     for label, (ratio, fpl, wpl, apl) in ratios.items():
         key = label.replace("-", "_")

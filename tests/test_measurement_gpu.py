@@ -15,9 +15,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def test_bench_prints_one_contract_line(device):
     cmd = [sys.executable, "-u", os.path.join(ROOT, "bench.py"), "--steps", "2", "--warmup", "1",
-           "--prewarm", "2", "--cpu-seconds", "0.5", "--resident-reps", "2"]
+           "--prewarm", "2", "--cpu-seconds", "0.5", "--resident-reps", "2",
+           "--config-steps", "2", "--layers", "2", "--context", "64", "--tree-nodes", "8",
+           "--expert-sets", "2"]
     print("bench contract run:", " ".join(cmd[2:]), flush=True)
-    out = subprocess.run(cmd, capture_output=True, text=True, timeout=110, cwd=ROOT)
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=170, cwd=ROOT)
     assert out.returncode == 0, out.stderr[-3000:]
     lines = [line for line in out.stdout.splitlines() if line.strip()]
     assert len(lines) == 1, out.stdout[-2000:]
@@ -48,6 +50,15 @@ def test_bench_prints_one_contract_line(device):
     assert raw["value"] == pytest.approx(2 * 64 / (raw["ms_per_step"] * 2e-3), rel=1e-6)
     assert raw["misses_per_step"] > 0 and raw["h2d_gbs"] > 0
     assert 0 < raw["k3_in_step_gbs"] < 8000.0
+    # the other configurations, each in a short run of its own
+    other = d["other_configs"]
+    assert set(other) == {"resident16", "sweep", "verify48", "cold48"}
+    assert all("error" not in v for v in other.values()), other
+    assert other["resident16"]["value"] > 0 and 0 < other["resident16"]["k3_frac"] < 1
+    assert [p["tokens"] for p in other["sweep"]["points"]] == [1, 8, 32, 64, 128]
+    assert all(p["tokens_per_s"] > 0 for p in other["sweep"]["points"])
+    for name in ("verify48", "cold48"):
+        assert other[name]["value"] > 0 and "2 layers" in other[name]["workload"]
 
 
 

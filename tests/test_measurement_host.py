@@ -64,6 +64,13 @@ def test_traffic_summary_calibrates_and_splits_phases(tmp_path):
         for kind, wb in (("gateup", GATEUP_BYTES), ("down", DOWN_BYTES)):
             fetch.append((_name(kind, nt), _grid(kind, nt, n), n * wb * 1.05 / 1024 / 2))
             write.append((_name(kind, nt), _grid(kind, nt, n), n * wb * 0.01 / 1024))
+    # two decodes of coded records: 1152 chunks of 4096 values, 6.3 MB read,
+    # every value written once
+    dec = "void (anonymous namespace)::decode_kernel((anonymous namespace)::DecodeArgs)"
+    values = 1152 * 4096
+    for _ in range(2):
+        fetch.append((dec, 1152 * pmc.THREADS, 6.3e6 / 1024 / 2))
+        write.append((dec, 1152 * pmc.THREADS, 2 * values / 1024))
     fetch.append((CAL, 1 << 20, cal_kib / 2))
     write.append((CAL, 1 << 20, cal_kib))
     for kind, wb in (("gateup", GATEUP_BYTES), ("down", DOWN_BYTES)):  # all-resident, 45 experts
@@ -76,6 +83,11 @@ def test_traffic_summary_calibrates_and_splits_phases(tmp_path):
     assert ratios["traffic_ratio_in_step"] == pytest.approx(1.06, abs=1e-6)
     assert ratios["traffic_ratio_all_resident"] == pytest.approx(1.02, abs=1e-6)
     assert "| FETCH_SIZE |" in text and "2.0000" in text and "    cmd" in text
+    dec_bytes = {line.split(":")[0]: float(line.split(":")[1]) for line in text.splitlines()
+                 if line.startswith("decode_")}
+    assert dec_bytes["decode_fetch_bytes"] == pytest.approx(6.3e6, rel=1e-9)
+    assert dec_bytes["decode_write_bytes"] == pytest.approx(2 * values, rel=1e-9)
+    assert "| 2 | 6.300 | 9.437 | 9.437 | 1.000 |" in text
 
 
 def test_traffic_summary_rejects_mismatched_runs(tmp_path):
