@@ -220,6 +220,7 @@ class Qwen3ExpertPrefetch:
         self._trace = trace
         self._log: list[dict] = []
         self._stack = ExitStack()
+        self._owned_streams: tuple = ()
         self._holds: dict[ExpertKey, _Hold] = {}
         self._copies: deque[_Hold] = deque()   # own transfers not yet seen complete, in order
         self._prior: list[torch.cuda.Event] = []  # incomplete transfers from before entry
@@ -255,11 +256,19 @@ class Qwen3ExpertPrefetch:
             dev = self._caches[0].device
             pair = (torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev))
             self._copy_stream, self._copy_pair = pair[0], pair
+            # Copies of the context start after every copy the caches queued
+            # before it (the layer caches of a model share one stream pair:
+            # each distinct stream is waited for once).
+            owned = {}
+            for cache in self._caches:
+                for s in (cache.copy_stream, cache._aux_copy_stream, cache._own_copy_stream):
+                    owned.setdefault(int(s.cuda_stream), s)
+            for earlier in owned.values():
+                for s in pair:
+                    s.wait_stream(earlier)
+            self._owned_streams = tuple(owned.values())
             for cache in self._caches:
                 own = (cache.copy_stream, cache._aux_copy_stream, cache._own_copy_stream)
-                for earlier in {id(s): s for s in own}.values():
-                    for s in pair:
-                        s.wait_stream(earlier)
                 # Transfers still running keep their queue credits.
                 self._prior += [t.ready_event for t in cache._outstanding_transfers
                                 if not t.ready_event.query()]
@@ -269,6 +278,9 @@ class Qwen3ExpertPrefetch:
                 cache.copy_stream, cache._aux_copy_stream = pair
                 cache._own_copy_stream = pair[0]
                 self._stack.callback(self._give_back_streams, cache, own)
+            # Runs first at exit (callbacks run last-in first-out): the
+            # caches' own streams wait for the context's copies, once each.
+            self._stack.callback(self._order_owned_streams)
             for lid, (layer, module) in enumerate(zip(self._layers, modules)):
                 module._prediction_scheduler = self
                 self._stack.callback(setattr, module, "_prediction_scheduler", None)
@@ -284,10 +296,13 @@ class Qwen3ExpertPrefetch:
             self._stack.close()
             raise
 
-    def _give_back_streams(self, cache, own) -> None:
-        for s in {id(s): s for s in own}.values():
+    def _order_owned_streams(self) -> None:
+        for s in self._owned_streams:
             for mine in self._copy_pair:
                 s.wait_stream(mine)
+
+    @staticmethod
+    def _give_back_streams(cache, own) -> None:
         cache.copy_stream, cache._aux_copy_stream, cache._own_copy_stream = own
 
     def __exit__(self, exc_type, exc, tb) -> None:
