@@ -12,7 +12,11 @@
 //
 // At verification sizes (Q = 61 tree tokens, S ~ 1.1k keys, 32 query heads,
 // 4 KV heads, head dim 128) the whole layer's K/V is ~2 MB: the kernel is
-// latency-bound, not HBM-bound.  One workgroup per (query, KV head) keeps the
+// latency-bound, not HBM-bound.  Head dims 64 and 128 with 2..16 query heads
+// per KV head run the MFMA form below (26 us at the 61-token verification
+// shape and 28 us at 128 tokens on MI355X, against 54 and 108 us for the
+// loop form).  The loop form covers every other shape: one workgroup per
+// (query, KV head) keeps the
 // G query heads of the group together so each K/V row is read once per
 // query.  Its 8 wavefronts take interleaved 64-key chunks: scores with one
 // key per lane (the key row in registers, the query rows broadcast from
@@ -272,6 +276,270 @@ __global__ __launch_bounds__(NW * SF_WAVE) void tree_attention_kernel(const Attn
   }
 }
 
+// ------------------------------------------------------- MFMA form --
+// For head dims 64 / 128 and 2..16 query heads per KV head, with 16-byte
+// aligned rows.  A workgroup owns one KV head and a tile of 16 query rows
+// (16 / G tokens x the G heads of the group) and all keys; its 8 wavefronts
+// take interleaved 32-key chunks.  Per chunk a wavefront computes the
+// 16 x 32 score tile with v_mfma_f32_16x16x32_bf16 (A = query rows, B = key
+// rows: both 8 consecutive head-dim elements per lane, straight from
+// memory), applies the scale and the mask, updates its online softmax per
+// row (rows 4 (l / 16) + i of lane l, reduced over the 16 lanes that share
+// them), and adds P.V with P (bf16) read back from LDS as the A operand and
+// the chunk's value rows staged in LDS (B: 8 keys of one head-dim column per
+// lane).  The 8 wavefront states are merged in wavefront order, so the
+// result is run-to-run identical.
+constexpr int kMfmaWaves = 8;
+constexpr int kKeysPerChunk = 32;
+constexpr int kPRow = kKeysPerChunk * 2 + 16;  // P row in LDS (bytes, padded)
+
+template <int D>
+constexpr int v_row_bytes() { return D * 2 + 8; }  // 8 B pad: the four 8-row groups hit distinct banks
+
+template <int D>
+constexpr size_t mfma_lds_bytes() {
+  constexpr size_t loop = kMfmaWaves * (kKeysPerChunk * v_row_bytes<D>() + 16 * kPRow);
+  constexpr size_t merge = kMfmaWaves * 16 * (D + 2) * sizeof(float);
+  return loop > merge ? loop : merge;
+}
+
+__device__ __forceinline__ sf_f32x4 mfma_bf16(uint4 a, uint4 b, sf_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sf_bf16x8, a),
+                                                 __builtin_bit_cast(sf_bf16x8, b), c, 0, 0, 0);
+}
+
+// Max / sum over the 16 lanes of a lane's row group (lanes 16 g .. 16 g + 15,
+// one DPP row): the group_sum moves, with max for the max.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float x) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false);
+  return fmaxf(x, __int_as_float(moved));
+}
+
+__device__ __forceinline__ float row16_max(float x) {
+  x = dpp_max<0xB1>(x);
+  x = dpp_max<0x4E>(x);
+  x = dpp_max<0x141>(x);
+  return dpp_max<0x140>(x);
+}
+
+__device__ __forceinline__ float row16_sum(float x) { return group_sum<16>(x); }
+
+template <int G, int D>
+__global__ __launch_bounds__(kMfmaWaves * SF_WAVE) void tree_attention_mfma_kernel(
+    const AttnArgs a) {
+  constexpr int kTok = 16 / G;        // tokens per 16-row tile
+  constexpr int kSteps = D / 32;      // MFMA k-steps of a score tile
+  constexpr int kNt = D / 16;         // 16-wide head-dim tiles of the output
+  constexpr int kVRow = v_row_bytes<D>();
+  __shared__ __attribute__((aligned(16))) char lds[mfma_lds_bytes<D>()];
+  const int lane = threadIdx.x & (SF_WAVE - 1);
+  const int wave = threadIdx.x / SF_WAVE;
+  const int g4 = lane >> 4;           // row group of the C layout / k group of A, B
+  const int col = lane & 15;
+  const int h = blockIdx.x % a.Hkv;
+  const int t0 = (blockIdx.x / a.Hkv) * kTok;
+  char* vtile = lds + wave * kKeysPerChunk * kVRow;                       // [32][D] bf16
+  char* ptile = lds + kMfmaWaves * kKeysPerChunk * kVRow + wave * 16 * kPRow;  // [16][32] bf16
+
+  // A operand: query row `col` of the tile (token t0 + col / G, head h G + col % G).
+  uint4 qa[kSteps];
+  {
+    const int t = min(t0 + col / G, a.Q - 1);
+    const uint16_t* qr = a.q + t * a.q_tok + static_cast<int64_t>(h * G + col % G) * a.q_head;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s)
+      qa[s] = *reinterpret_cast<const uint4*>(qr + 32 * s + 8 * g4);
+  }
+  // Rows of this lane in the C layout: 4 g4 + i, token t0 + (4 g4 + i) / G.
+  int tok[4];
+  bool row_ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    tok[i] = t0 + (4 * g4 + i) / G;
+    row_ok[i] = tok[i] < a.Q;
+  }
+  const uint16_t* kh = a.k + h * a.k_head;
+  const uint16_t* vh = a.v + h * a.v_head;
+  float m[4], l[4];
+  sf_f32x4 acc[kNt];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+  }
+#pragma unroll
+  for (int nt = 0; nt < kNt; ++nt) acc[nt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Chunk loads (keys, value rows, mask bits) are issued one chunk ahead.
+  constexpr int kLanesPerRow = D / 8;
+  constexpr int kRowsPerLoad = SF_WAVE / kLanesPerRow;
+  constexpr int kVLoads = kKeysPerChunk / kRowsPerLoad;
+  constexpr int kStride = kMfmaWaves * kKeysPerChunk;
+  uint4 kf[2][kSteps], vv[kVLoads];
+  uint32_t okbits = 0;  // bit 4 ct + i: key kb + 16 ct + col admitted for row 4 g4 + i
+  auto load_chunk = [&](int kb) {
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      // Key fragments (B): key kb + 16 ct + col, head-dim 32 s + 8 g4.
+      const uint16_t* kr = kh + min(kb + 16 * ct + col, a.S - 1) * a.k_tok + 8 * g4;
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) kf[ct][s] = *reinterpret_cast<const uint4*>(kr + 32 * s);
+    }
+    // Value rows kb .. kb + 31 (rows past the end repeat the last key: finite
+    // values that meet p = 0).
+#pragma unroll
+    for (int j = 0; j < kVLoads; ++j) {
+      const int r = j * kRowsPerLoad + lane / kLanesPerRow;
+      vv[j] = *reinterpret_cast<const uint4*>(vh + min(kb + r, a.S - 1) * a.v_tok +
+                                              8 * (lane % kLanesPerRow));
+    }
+    okbits = 0;
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int key = kb + 16 * ct + col;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // Rows of one token share its mask byte (consecutive rows 4 g4 + i).
+        bool ok = row_ok[i] && key < a.S;
+        if (ok) ok = a.mask ? a.mask[tok[i] * a.mask_q + key] != 0 : key <= a.S - a.Q + tok[i];
+        okbits |= static_cast<uint32_t>(ok) << (4 * ct + i);
+      }
+    }
+  };
+  if (wave * kKeysPerChunk < a.S) load_chunk(wave * kKeysPerChunk);
+  for (int kb = wave * kKeysPerChunk; kb < a.S; kb += kStride) {
+    uint4 kc[2][kSteps];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) kc[ct][s] = kf[ct][s];
+    const uint32_t okc = okbits;
+    // The chunk's value rows into this wavefront's LDS tile.
+#pragma unroll
+    for (int j = 0; j < kVLoads; ++j) {
+      const int r = j * kRowsPerLoad + lane / kLanesPerRow;
+      uint2* dst = reinterpret_cast<uint2*>(vtile + r * kVRow + 16 * (lane % kLanesPerRow));
+      dst[0] = make_uint2(vv[j].x, vv[j].y);
+      dst[1] = make_uint2(vv[j].z, vv[j].w);
+    }
+    if (kb + kStride < a.S) load_chunk(kb + kStride);
+    // Scores of the 16 x 32 tile.
+    sf_f32x4 sc[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      sc[ct] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) sc[ct] = mfma_bf16(qa[s], kc[ct][s], sc[ct]);
+    }
+    // Online softmax per row.
+    float p[2][4];
+    float alpha[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bool ok[2];
+      float x[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        ok[ct] = (okc >> (4 * ct + i)) & 1u;
+        x[ct] = sc[ct][i] * a.scale;
+      }
+      const float cmax = row16_max(fmaxf(ok[0] ? x[0] : -INFINITY, ok[1] ? x[1] : -INFINITY));
+      const float mnew = fmaxf(m[i], cmax);
+      alpha[i] = 1.f;
+      p[0][i] = p[1][i] = 0.f;
+      if (mnew != -INFINITY) {
+        alpha[i] = m[i] == -INFINITY ? 0.f : __expf(m[i] - mnew);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+          if (ok[ct]) p[ct][i] = __expf(x[ct] - mnew);
+      }
+      l[i] = l[i] * alpha[i] + row16_sum(p[0][i] + p[1][i]);
+      m[i] = mnew;
+    }
+#pragma unroll
+    for (int nt = 0; nt < kNt; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[nt][i] *= alpha[i];
+    // P (bf16) through LDS into the A layout: row col, keys 8 g4 .. 8 g4 + 7.
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint16_t*>(ptile + (4 * g4 + i) * kPRow + 2 * (16 * ct + col)) =
+            sf_f32_to_bf16(p[ct][i]);
+    // The V and P tiles are this wavefront's own: its LDS accesses run in
+    // order, and the fence keeps the compiler from moving the reads above.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const uint4 pa = *reinterpret_cast<const uint4*>(ptile + col * kPRow + 16 * g4);
+    // P.V: B = value rows 8 g4 .. 8 g4 + 7 of head-dim column 16 nt + col.
+#pragma unroll
+    for (int nt = 0; nt < kNt; ++nt) {
+      uint32_t w[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const char* v0 = vtile + (8 * g4 + 2 * jj) * kVRow + 2 * (16 * nt + col);
+        const uint32_t lo = *reinterpret_cast<const uint16_t*>(v0);
+        const uint32_t hi = *reinterpret_cast<const uint16_t*>(v0 + kVRow);
+        w[jj] = lo | (hi << 16);
+      }
+      acc[nt] = mfma_bf16(pa, make_uint4(w[0], w[1], w[2], w[3]), acc[nt]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // tiles reused by the next chunk
+  }
+
+  // Merge the wavefront states in wavefront order.  The merge state overlays
+  // the tiles of every wavefront: all of them have left the chunk loop first.
+  __syncthreads();
+  float* mst = reinterpret_cast<float*>(lds);                        // [waves][16] max
+  float* lst = mst + kMfmaWaves * 16;                                 // [waves][16] sum
+  float* ast = lst + kMfmaWaves * 16;                                 // [waves][16][D] acc
+  if (col == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mst[wave * 16 + 4 * g4 + i] = m[i];
+      lst[wave * 16 + 4 * g4 + i] = l[i];
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < kNt; ++nt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ast[(wave * 16 + 4 * g4 + i) * D + 16 * nt + col] = acc[nt][i];
+  __syncthreads();
+  const int Hq = a.Hkv * G;
+  for (int o = threadIdx.x; o < 16 * D; o += kMfmaWaves * SF_WAVE) {
+    const int r = o / D;
+    const int d = o - r * D;
+    const int t = t0 + r / G;
+    if (t >= a.Q) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kMfmaWaves; ++w) M = fmaxf(M, mst[w * 16 + r]);
+    float L = 0.f, O = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kMfmaWaves; ++w) {
+        const float mw = mst[w * 16 + r];
+        if (mw == -INFINITY) continue;
+        const float f = __expf(mw - M);
+        L = __builtin_fmaf(lst[w * 16 + r], f, L);
+        O = __builtin_fmaf(ast[(w * 16 + r) * D + d], f, O);
+      }
+    }
+    const float out = L > 0.f ? O / L : 0.f;
+    a.out[(static_cast<int64_t>(t) * Hq + h * G + r % G) * D + d] = sf_f32_to_bf16(out);
+  }
+}
+
+template <int G, int D>
+int launch_mfma(const AttnArgs& a, hipStream_t s) {
+  constexpr int kTok = 16 / G;
+  const dim3 grid(static_cast<unsigned>((a.Q + kTok - 1) / kTok) * a.Hkv);
+  tree_attention_mfma_kernel<G, D><<<grid, dim3(kMfmaWaves * SF_WAVE), 0, s>>>(a);
+  SF_LAUNCH_CHECK();
+  return SF_OK;
+}
+
 // Wavefronts per workgroup: 8 up to 8 heads per group, 4 for 16 (LDS).
 constexpr int waves_for(int G) { return G <= 8 ? 8 : 4; }
 
@@ -353,6 +621,28 @@ extern "C" int sf_tree_attention(const void* q, int64_t q_stride_token, int64_t 
   a.scale = scale;
   a.out = static_cast<uint16_t*>(out);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // The MFMA form: 16-byte aligned query / key / value rows (8-element
+  // strides), head dim 64 or 128, 2..16 query heads per KV head.
+  const bool rows16 = aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
+                      q_stride_token % 8 == 0 && q_stride_head % 8 == 0 &&
+                      v_stride_token % 8 == 0 && v_stride_head % 8 == 0;
+  if (rows16 && head_dim == 128) {
+    switch (G) {
+      case 2: return launch_mfma<2, 128>(a, s);
+      case 4: return launch_mfma<4, 128>(a, s);
+      case 8: return launch_mfma<8, 128>(a, s);
+      case 16: return launch_mfma<16, 128>(a, s);
+      default: break;
+    }
+  } else if (rows16 && head_dim == 64) {
+    switch (G) {
+      case 2: return launch_mfma<2, 64>(a, s);
+      case 4: return launch_mfma<4, 64>(a, s);
+      case 8: return launch_mfma<8, 64>(a, s);
+      case 16: return launch_mfma<16, 64>(a, s);
+      default: break;
+    }
+  }
   switch (G) {
     case 1: return launch_g<1>(a, s);
     case 2: return launch_g<2>(a, s);

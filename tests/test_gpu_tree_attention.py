@@ -68,6 +68,7 @@ def test_verification_shape_with_tree_mask(device):
 
 @pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 8), (4, 2, 8), (8, 2, 64), (16, 4, 128),
                                       (16, 1, 128), (32, 4, 96), (8, 2, 256),
+                                      (32, 4, 128), (8, 4, 64), (8, 4, 128), (32, 2, 64),
                                       (64, 4, 128)])  # the last: Qwen3-235B-A22B attention
 @pytest.mark.parametrize("Q,S", [(1, 1), (1, 300), (7, 7), (61, 1085), (130, 130)])
 def test_shapes_causal_and_masked(device, Hq, Hkv, D, Q, S):
@@ -83,6 +84,32 @@ def test_shapes_causal_and_masked(device, Hq, Hkv, D, Q, S):
     mask = (torch.rand((1, 1, Q, S), generator=gm) < 0.3).to(device)
     mask[..., 0] = True
     _check(ops.tree_attention(q, k, v, mask, scale), _reference(q, k, v, mask, scale))
+
+
+def test_mfma_and_loop_kernels_agree(device):
+    """The verification shape through the MFMA kernel (16-byte aligned rows)
+    and through the loop kernel (a query view one element off alignment):
+    both within the fp32 reference's tolerance, and within bf16 rounding of
+    each other."""
+    g = torch.Generator().manual_seed(12)
+    tree = synthetic_tree(60, 6, seed=6, vocab=151936)
+    base, Q, Hq, Hkv, D = 1024, 61, 32, 4, 128
+    S = base + Q
+    qbuf = _rand((1, Q, Hq, D + 8), device, g)
+    q_aligned = qbuf[..., :D].transpose(1, 2)
+    q_shifted = torch.empty((1, Q, Hq, D + 1), dtype=torch.bfloat16, device=device)
+    q_shifted[..., 1:] = qbuf[..., :D]
+    q_off = q_shifted[..., 1:].transpose(1, 2)  # same values, rows 2 bytes off alignment
+    k = _rand((1, Hkv, S, D), device, g)
+    v = _rand((1, Hkv, S, D), device, g)
+    mask = tree.verification_attention_mask(base_kv_length=base, device=device)
+    scale = D ** -0.5
+    ref = _reference(q_aligned, k, v, mask, scale)
+    fast = ops.tree_attention(q_aligned, k, v, mask, scale)
+    loop = ops.tree_attention(q_off, k, v, mask, scale)
+    _check(fast, ref)
+    _check(loop, ref)
+    assert ((fast.float() - loop.float()).abs().max() / ref.abs().max()).item() <= 1e-2
 
 
 def test_fully_masked_row_is_zero_and_large_logits_are_stable(device):
