@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 12
+#define SF_ABI_VERSION 13
 
 /* Argument error codes (hipError_t values are returned as SF_ERR_HIP_BASE + e). */
 #define SF_OK 0
@@ -346,14 +346,18 @@ int sf_rms_norm(const void *x, int64_t row_stride, int rows, int dim,
  *   n = sf_rms_norm's row result (same bits)
  *   out[h, t, d] = bf16(bf16(n[d] * cos[t, d]) + bf16(rot(n)[d] * sin[t, d]))
  *   rot(n)[d] = -n[d + D/2] for d < D/2, n[d - D/2] otherwise
- *   q, k        bf16 [tokens, q_heads | kv_heads, head_dim], contiguous
+ *   q, k        bf16 [tokens, q_heads | kv_heads, head_dim]: token t at
+ *               q + t * q_stride_token (elements; >= q_heads * head_dim and a
+ *               multiple of 8, e.g. one fused q/k/v projection row), heads
+ *               contiguous within a token
  *   q_weight, k_weight  bf16 [head_dim]
  *   cos, sin    bf16 [tokens, head_dim], contiguous
  *   q_out, k_out  bf16 [q_heads | kv_heads, tokens, head_dim], contiguous
  * head_dim must be 128 (SF_ERR_UNSUPPORTED_SHAPE otherwise); all buffers
  * 16-byte aligned.
  */
-int sf_qk_norm_rope(const void *q, const void *k, int tokens, int q_heads,
+int sf_qk_norm_rope(const void *q, int64_t q_stride_token, const void *k,
+                    int64_t k_stride_token, int tokens, int q_heads,
                     int kv_heads, int head_dim, const void *q_weight,
                     const void *k_weight, float eps, const void *cos,
                     const void *sin, void *q_out, void *k_out,

@@ -10,7 +10,7 @@ import threading
 
 from .build import LIB_PATH
 
-SF_ABI_VERSION = 12
+SF_ABI_VERSION = 13
 SF_ERR_HIP_BASE = 1000
 
 _lock = threading.Lock()
@@ -40,7 +40,8 @@ SIGNATURES = {
     "sf_tree_attention": ([_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64,
                            _i, _i, _i, _i, _i, ctypes.c_float, _p, _p], _i),
     "sf_rms_norm": ([_p, _i64, _i, _i, _p, ctypes.c_float, _p, _i64, _p], _i),
-    "sf_qk_norm_rope": ([_p, _p, _i, _i, _i, _i, _p, _p, ctypes.c_float, _p, _p, _p, _p, _p], _i),
+    "sf_qk_norm_rope": ([_p, _i64, _p, _i64, _i, _i, _i, _i, _p, _p, ctypes.c_float, _p, _p, _p,
+                         _p, _p], _i),
 }
 
 

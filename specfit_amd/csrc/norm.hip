@@ -154,7 +154,8 @@ __device__ __forceinline__ float row16_sum(float x) {
 }
 
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, int tokens, int q_heads,
+    const uint16_t* __restrict__ q, int64_t q_tok, const uint16_t* __restrict__ k, int64_t k_tok,
+    int tokens, int q_heads,
     int kv_heads, const uint16_t* __restrict__ wq, const uint16_t* __restrict__ wk, float eps,
     const uint16_t* __restrict__ cos, const uint16_t* __restrict__ sin,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out) {
@@ -172,7 +173,8 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
   const int heads = is_q ? q_heads : kv_heads;
   const int t = rr / heads;
   const int h = rr - t * heads;
-  const uint16_t* src = (is_q ? q : k) + static_cast<int64_t>(rr) * kRopeDim;
+  const uint16_t* src = (is_q ? q : k) + static_cast<int64_t>(t) * (is_q ? q_tok : k_tok) +
+                        static_cast<int64_t>(h) * kRopeDim;
   const uint16_t* w = is_q ? wq : wk;
   float f[8], g[8], c[8], s[8];
   unpack(ld16(src + 8 * j), f);
@@ -209,12 +211,17 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
 
 }  // namespace
 
-extern "C" int sf_qk_norm_rope(const void* q, const void* k, int tokens, int q_heads,
+extern "C" int sf_qk_norm_rope(const void* q, int64_t q_stride_token, const void* k,
+                               int64_t k_stride_token, int tokens, int q_heads,
                                int kv_heads, int head_dim, const void* q_weight,
                                const void* k_weight, float eps, const void* cos, const void* sin,
                                void* q_out, void* k_out, sf_stream_t stream) {
   if (tokens < 0 || q_heads < 1 || kv_heads < 1 || !(eps >= 0.f)) return SF_ERR_INVALID_ARGUMENT;
   if (head_dim != kRopeDim) return SF_ERR_UNSUPPORTED_SHAPE;
+  if (q_stride_token < static_cast<int64_t>(q_heads) * kRopeDim ||
+      k_stride_token < static_cast<int64_t>(kv_heads) * kRopeDim || q_stride_token % 8 ||
+      k_stride_token % 8)
+    return SF_ERR_INVALID_ARGUMENT;
   if (tokens == 0) return SF_OK;
   const void* ptrs[] = {q, k, q_weight, k_weight, cos, sin, q_out, k_out};
   for (const void* p : ptrs)
@@ -223,7 +230,8 @@ extern "C" int sf_qk_norm_rope(const void* q, const void* k, int tokens, int q_h
   if (rows > 0x7fffffffLL / 16) return SF_ERR_UNSUPPORTED_SHAPE;
   const unsigned blocks = static_cast<unsigned>((rows * 16 + kThreads - 1) / kThreads);
   qk_norm_rope_kernel<<<dim3(blocks), dim3(kThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), tokens, q_heads, kv_heads,
+      static_cast<const uint16_t*>(q), q_stride_token, static_cast<const uint16_t*>(k),
+      k_stride_token, tokens, q_heads, kv_heads,
       static_cast<const uint16_t*>(q_weight), static_cast<const uint16_t*>(k_weight), eps,
       static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
       static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out));

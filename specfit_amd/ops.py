@@ -726,26 +726,35 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
     """Query/key RMSNorm + rotary embedding of one attention layer (K7).
 
     q [1, T, Hq, 128] and k [1, T, Hk, 128] bf16 (the projections viewed per
-    head, contiguous), norm weights bf16 [128], cos/sin bf16 [1, T, 128].
+    head: heads contiguous within a token, tokens at any stride that is a
+    multiple of 8, such as views into one fused q/k/v projection), norm
+    weights bf16 [128], cos/sin bf16 [1, T, 128] contiguous.
     Returns (q, k) as [1, Hq, T, 128] and [1, Hk, T, 128] contiguous: the
     tensors Qwen3MoeAttention.forward has after its norms, transposes and
     apply_rotary_pos_emb, with the same bits when the norms are K6's."""
     for name, t in (("q", q), ("k", k), ("q_weight", q_weight), ("k_weight", k_weight),
                     ("cos", cos), ("sin", sin)):
         _require_cuda(name, t, _BF16)
+    for name, t in (("q_weight", q_weight), ("k_weight", k_weight), ("cos", cos), ("sin", sin)):
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous")
     if q.dim() != 4 or k.dim() != 4 or q.shape[0] != 1 or k.shape[:2] != q.shape[:2]:
         raise ValueError("q and k must be [1, tokens, heads, head_dim] with the same tokens")
     _, T, Hq, D = q.shape
     Hk = k.shape[2]
+    for name, t in (("q", q), ("k", k)):
+        if t.stride(3) != 1 or t.stride(2) != D or (T > 1 and t.stride(1) % 8):
+            raise ValueError(f"{name} must have contiguous heads and a token stride that is a "
+                             "multiple of 8")
     if k.shape[3] != D or q_weight.shape != (D,) or k_weight.shape != (D,):
         raise ValueError("head dimensions do not match")
     if cos.shape != (1, T, D) or sin.shape != (1, T, D):
         raise ValueError(f"cos and sin must be [1, {T}, {D}]")
     q_out = torch.empty((1, Hq, T, D), dtype=_BF16, device=q.device)
     k_out = torch.empty((1, Hk, T, D), dtype=_BF16, device=q.device)
-    rc = _native.lib().sf_qk_norm_rope(q.data_ptr(), k.data_ptr(), T, Hq, Hk, D,
+    q_tok = q.stride(1) if T > 1 else Hq * D
+    k_tok = k.stride(1) if T > 1 else Hk * D
+    rc = _native.lib().sf_qk_norm_rope(q.data_ptr(), q_tok, k.data_ptr(), k_tok, T, Hq, Hk, D,
                                        q_weight.data_ptr(), k_weight.data_ptr(), float(eps),
                                        cos.data_ptr(), sin.data_ptr(), q_out.data_ptr(),
                                        k_out.data_ptr(), _stream_handle(stream, q.device))

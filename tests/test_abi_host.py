@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_error_strings():
-    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 12
+    assert _native.lib().sf_abi_version() == _native.SF_ABI_VERSION == 13
     assert _native.error_string(0) == "success"
     assert _native.error_string(1) == "invalid argument"
     assert _native.error_string(12345) != ""
@@ -73,6 +73,15 @@ def test_host_side_validation_needs_no_device():
     assert attn(32, 4, 512) == 2
     assert attn(96, 4, 128) == 2          # 24 query heads per key/value head
     assert attn(32, 4, 128, k=fake + 8) == 3
+    # query/key norm + rotary: head dim, token strides shorter than the heads or unaligned
+    def qk(q_tok, k_tok, head_dim=128, tokens=2):
+        return lib.sf_qk_norm_rope(fake, q_tok, fake, k_tok, tokens, 32, 4, head_dim, fake, fake,
+                                   1e-6, fake, fake, fake, fake, null)
+    assert qk(4096, 512, head_dim=64) == 2
+    assert qk(4095, 512) == 1
+    assert qk(4096, 511) == 1
+    assert qk(5124, 5120) == 1
+    assert qk(5120, 5120, tokens=0) == 0
     assert lib.sf_copy_h2d(null, null, 0, null) == 0
     assert lib.sf_copy_h2d(null, null, 16, null) == 1
 

@@ -133,6 +133,35 @@ def test_qk_norm_rope_equals_the_eager_sequence_bitwise(device, tokens):
     assert torch.equal(aq, eq) and torch.equal(ak, ek)
 
 
+@pytest.mark.parametrize("tokens", [1, 5, 64])
+def test_qk_norm_rope_reads_heads_out_of_fused_projection_rows(device, tokens):
+    """q and k as views into one [tokens, (Hq + 2 Hk) * 128] projection
+    output (token stride 5120 elements, like Qwen3-30B-A3B's fused q/k/v
+    rows) give the bits of the same heads copied out contiguously."""
+    torch.manual_seed(100 + tokens)
+    Hq, Hk, D = 32, 4, 128
+    rows = (torch.randn(1, tokens, (Hq + 2 * Hk) * D, device=device) * 2).to(torch.bfloat16)
+    q = rows[..., :Hq * D].view(1, tokens, Hq, D)
+    k = rows[..., Hq * D:(Hq + Hk) * D].view(1, tokens, Hk, D)
+    assert not q.is_contiguous() or tokens == 1
+    wq = (1 + 0.2 * torch.randn(D, device=device)).to(torch.bfloat16)
+    wk = (1 + 0.2 * torch.randn(D, device=device)).to(torch.bfloat16)
+    ang = torch.rand(1, tokens, D, device=device) * 6.2
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    aq, ak = ops.qk_norm_rope(q, k, wq, wk, 1e-6, cos, sin)
+    eq, ek = ops.qk_norm_rope(q.contiguous(), k.contiguous(), wq, wk, 1e-6, cos, sin)
+    assert torch.equal(aq, eq) and torch.equal(ak, ek)
+
+
+def test_qk_norm_rope_rejects_unaligned_token_strides(device):
+    rows = torch.zeros(1, 3, 4 * 128 + 4, dtype=torch.bfloat16, device=device)
+    q = rows[..., :4 * 128].view(1, 3, 4, 128)
+    w = torch.ones(128, dtype=torch.bfloat16, device=device)
+    cs = torch.zeros(1, 3, 128, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        ops.qk_norm_rope(q, q, w, w, 1e-6, cs, cs)
+
+
 @pytest.mark.parametrize("head_dim", [128, 64])
 def test_hip_attention_module_matches_the_hf_module(device, head_dim):
     """Qwen3AttentionHip (fused at head_dim 128, eager norms+rotary at 64)
@@ -155,6 +184,34 @@ def test_hip_attention_module_matches_the_hf_module(device, head_dim):
     h = torch.randn(1, T, 256, device=device).to(torch.bfloat16)
     pos = torch.arange(T, device=device).unsqueeze(0)
     emb = Qwen3MoeRotaryEmbedding(cfg).to(device)(h, pos)
+    mask = torch.tril(torch.ones(T, T, dtype=torch.bool, device=device)).view(1, 1, T, T)
+    assert hip._fused_projection()
+    with torch.no_grad():
+        expected, _ = hf(h, emb, mask)
+        actual, _ = hip(h, emb, mask)
+    assert torch.equal(actual, expected)
+
+
+def test_replaced_projection_weight_turns_the_fused_projection_off(device):
+    """A q_proj weight replaced after wrapping is the one used: the layer
+    falls back to three GEMMs and still matches the HF module."""
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import (Qwen3MoeAttention,
+                                                                    Qwen3MoeRotaryEmbedding)
+
+    from specfit_amd.runtime import Qwen3AttentionHip
+
+    torch.manual_seed(7)
+    cfg = _attention_config(128)
+    hf = Qwen3MoeAttention(cfg, layer_idx=0).to(device=device, dtype=torch.bfloat16).eval()
+    hf.q_norm = Qwen3RMSNormHip.from_module(hf.q_norm)
+    hf.k_norm = Qwen3RMSNormHip.from_module(hf.k_norm)
+    hip = Qwen3AttentionHip.from_module(hf)
+    assert hip._fused_projection()
+    hf.q_proj.weight = torch.nn.Parameter(torch.randn_like(hf.q_proj.weight))
+    assert not hip._fused_projection()
+    T = 5
+    h = torch.randn(1, T, 256, device=device).to(torch.bfloat16)
+    emb = Qwen3MoeRotaryEmbedding(cfg).to(device)(h, torch.arange(T, device=device)[None])
     mask = torch.tril(torch.ones(T, T, dtype=torch.bool, device=device)).view(1, 1, T, T)
     with torch.no_grad():
         expected, _ = hf(h, emb, mask)
