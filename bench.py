@@ -24,7 +24,11 @@ with HIP events: the roofline, H2D, overlap and link-busy figures come from
 it, and so do the per-step device times (K1 start to K4 end, H2D waits
 included; median and 10th/90th percentile in `device_ms_per_step`).
 --record none skips it.  Steps per pass default to 50 (10 for the 48-layer
-forwards).
+forwards).  With --record copies the 48-layer recorded pass also times
+every copy and marks every layer's router, and ``link`` splits the time the
+host link idles into the gaps at layer boundaries (waiting for the next
+layer's routing) and those inside a layer, with how long one or two copies
+ran; those events slow the recorded pass, so its split is indicative.
 
 The default single-layer run also reports, in the same line: a second
 measurement of the same workload whose misses copy the raw bf16 expert bytes
@@ -114,9 +118,12 @@ def parse_args(argv=None):
                         "configurations (other_configs: resident16, sweep, verify48, cold48)")
     p.add_argument("--config-steps", type=int, default=20,
                    help="steps per pass of the resident16 and sweep runs in other_configs")
-    p.add_argument("--record", choices=("full", "k3", "none"), default="full",
+    p.add_argument("--record", choices=("full", "k3", "none", "copies"), default="full",
                    help="timing events of the recorded pass: K3 launches + one copy window "
-                        "per step (full), K3 only, or none (no recorded pass)")
+                        "per step (full), K3 only, or none (no recorded pass); copies (the "
+                        "48-layer forwards): full plus an event pair around every copy and one "
+                        "at every layer's router, for the link breakdown (the extra events slow "
+                        "the recorded pass's host by 20-45%%)")
     args = p.parse_args(argv)
     if args.executor != "layer" and args.workload not in ("verify48", "cold48"):
         p.error("--executor applies to the 48-layer forwards (verify48, cold48)")
@@ -207,6 +214,64 @@ def _union_length(spans) -> float:
     if cur_e is not None:
         total += cur_e - cur_s
     return total
+
+
+def link_stats(rec, step_events) -> dict | None:
+    """Where the host link idles in the recorded 48-layer forwards, from a
+    (start, end) event pair around every copy and an event at every layer's
+    router.  Per forward: the union of the copy intervals, its gaps split
+    into those that contain a router event of layers 1.. (the layer
+    boundary: the link waits for the next layer's routing) and the rest
+    (inside a layer), the time before the first copy and after the last
+    one, and how long one copy or two copies at once were running."""
+    if not rec.copy_spans or not rec.marks or not step_events:
+        return None
+    origin = step_events[0][0]
+    t = lambda ev: origin.elapsed_time(ev) * 1e3  # us
+    spans = sorted((t(a), t(b)) for a, b in rec.copy_spans)
+    marks = [(label, t(ev)) for label, ev in rec.marks]
+    steps = [(t(a), t(b)) for a, b in step_events]
+    per = {"boundary_us": [], "boundary": 0.0, "within": 0.0, "prologue": 0.0, "epilogue": 0.0,
+           "one": 0.0, "two": 0.0, "busy": 0.0}
+    for s0, s1 in steps:
+        sp = [c for c in spans if s0 <= c[0] < s1]
+        if not sp:
+            continue
+        gaps, cur_e = [], sp[0][1]
+        for a, b in sp[1:]:
+            if a > cur_e:
+                gaps.append((cur_e, a))
+            cur_e = max(cur_e, b)
+        per["prologue"] += sp[0][0] - s0
+        per["epilogue"] += max(0.0, s1 - cur_e)
+        bounds = [m for label, m in marks if s0 <= m < s1 and label != 0]
+        at_boundary = set()
+        for m in bounds:
+            hit = next((g for g in gaps if g[0] <= m < g[1]), None)
+            per["boundary_us"].append(0.0 if hit is None else hit[1] - hit[0])
+            if hit is not None:
+                at_boundary.add(hit)
+        per["boundary"] += sum(b - a for a, b in at_boundary)
+        per["within"] += sum(b - a for a, b in gaps if (a, b) not in at_boundary)
+        edges = sorted([(a, 1) for a, _ in sp] + [(b, -1) for _, b in sp])
+        active, last = 0, edges[0][0]
+        for x, d in edges:
+            if active == 1:
+                per["one"] += x - last
+            elif active >= 2:
+                per["two"] += x - last
+            if active:
+                per["busy"] += x - last
+            active, last = active + d, x
+    n = len(steps)
+    b = sorted(per["boundary_us"])
+    return {"forwards": n, "copies": len(spans),
+            "boundary_idle_us": {"median": b[len(b) // 2], "mean": sum(b) / len(b),
+                                 "p90": b[min(len(b) - 1, 9 * len(b) // 10)],
+                                 "boundaries": len(b)} if b else None,
+            "ms_per_forward": {k: per[k] / n / 1e3 for k in
+                               ("busy", "one", "two", "boundary", "within", "prologue",
+                                "epilogue")}}
 
 
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -368,8 +433,16 @@ def main_verify(args) -> dict:
         rec = ops.LaunchRecorder(copies=False)
         rec_wall, rec_misses = 0.0, 0
         if recorded:
-            with ops.record_launches(copies=True, park_cycles=PARK_CYCLES) as rec:
-                rec_wall, rec_misses, _, _ = run_steps(args.warmup + args.steps, rec)
+            with ops.record_launches(copies=True, park_cycles=PARK_CYCLES,
+                                     per_copy=args.record == "copies") as rec:
+                marks = [layer.mlp.gate.register_forward_pre_hook(
+                             lambda mod, inp, l=l: rec.mark(l, compute))
+                         for l, layer in enumerate(target.model.layers)]
+                try:
+                    rec_wall, rec_misses, _, _ = run_steps(args.warmup + args.steps, rec)
+                finally:
+                    for h in marks:
+                        h.remove()
     H = config.hidden_size
     k3 = [(nx, rows, tag, s_.elapsed_time(e_) * 1e-3) for nx, rows, tag, s_, e_ in rec.k3]
     k3_time = sum(x[3] for x in k3)
@@ -424,6 +497,7 @@ def main_verify(args) -> dict:
                   "hits_per_layer": hits / (args.steps * args.layers)},
         "accepted_per_step": accepted / args.steps,
         "decode": decode_stats(rec),
+        "link": link_stats(rec, step_events),
     }
     if sched_stats:  # the timed pass's forwards
         timed = sched_stats[args.warmup:args.warmup + args.steps]
@@ -526,7 +600,7 @@ def main_sweep(args) -> dict:
         rec = ops.LaunchRecorder(copies=False)
         rec_wall, rec_misses = 0.0, 0
         if recorded:
-            with ops.record_launches(copies=args.record == "full", park_cycles=PARK_CYCLES) as rec:
+            with ops.record_launches(copies=args.record in ("full", "copies"), park_cycles=PARK_CYCLES) as rec:
                 rec_wall, rec_misses, _, _ = run_steps(hidden[base + args.steps:], rec)
         ms = []
         for idx in idxs:
@@ -725,7 +799,7 @@ def _layer_pass(args, dev, layer, router, hidden, image, *, resident: bool) -> d
     rec = ops.LaunchRecorder(copies=False)
     rec_wall, rec_misses = 0.0, 0
     if args.record != "none":
-        with ops.record_launches(copies=args.record == "full", park_cycles=PARK_CYCLES) as rec:
+        with ops.record_launches(copies=args.record in ("full", "copies"), park_cycles=PARK_CYCLES) as rec:
             rec_wall, rec_misses, _ = run_steps(hidden[base + args.steps:], rec)
         log(f"recorded {args.steps} steps in {rec_wall * 1e3:.2f} ms: {rec_misses} misses")
     torch.cuda.synchronize()

@@ -121,7 +121,8 @@ class LaunchRecorder:
     the stream the work runs on (enabled by ``record_launches``).  Events
     are TimingEvents; read them after the device has finished the work."""
 
-    def __init__(self, *, copies: bool = True, park_cycles: int = 0) -> None:
+    def __init__(self, *, copies: bool = True, park_cycles: int = 0,
+                 per_copy: bool = False) -> None:
         self.k3: list[tuple[int, int, str, TimingEvent, TimingEvent]] = []
         # With park_cycles, a short device sleep is queued on the stream
         # before each launch's start event: a launch enqueued while its
@@ -139,6 +140,13 @@ class LaunchRecorder:
         self.decodes: list[tuple[int, int, TimingEvent, TimingEvent]] = []
         self.windows: list[tuple[TimingEvent, TimingEvent]] = []
         self._open: dict[int, tuple[torch.cuda.Stream, TimingEvent]] = {}
+        # With per_copy, a (start, end) event pair on the copy stream around
+        # every copy, and ``mark`` events the caller records (e.g. at each
+        # layer's router) to place the copies in the forward.
+        self.per_copy = per_copy
+        self.copy_spans: list[tuple[TimingEvent, TimingEvent]] = []
+        self.marks: list[tuple[object, TimingEvent]] = []
+        self._copy_start: TimingEvent | None = None
 
     def _copy_started(self, stream: torch.cuda.Stream, nbytes: int) -> None:
         self.h2d_bytes += nbytes
@@ -148,6 +156,22 @@ class LaunchRecorder:
             start = TimingEvent()
             start.record(stream)
             self._open[key] = (stream, start)
+        if self.per_copy:
+            self._copy_start = TimingEvent()
+            self._copy_start.record(stream)
+
+    def _copy_ended(self, stream: torch.cuda.Stream) -> None:
+        if self.per_copy and self._copy_start is not None:
+            end = TimingEvent()
+            end.record(stream)
+            self.copy_spans.append((self._copy_start, end))
+            self._copy_start = None
+
+    def mark(self, label, stream: torch.cuda.Stream) -> None:
+        """Record an event labelled ``label`` on ``stream``."""
+        ev = TimingEvent()
+        ev.record(stream)
+        self.marks.append((label, ev))
 
     def close_copy_window(self) -> None:
         for stream, start in self._open.values():
@@ -194,15 +218,18 @@ _recorder: LaunchRecorder | None = None
 class record_launches:
     """Context manager: ``with record_launches() as rec: ...``."""
 
-    def __init__(self, *, copies: bool = True, park_cycles: int = 0) -> None:
+    def __init__(self, *, copies: bool = True, park_cycles: int = 0,
+                 per_copy: bool = False) -> None:
         self._copies = copies
         self._park = park_cycles
+        self._per_copy = per_copy
 
     def __enter__(self) -> LaunchRecorder:
         global _recorder
         if _recorder is not None:
             raise RuntimeError("launch recording is already active")
-        _recorder = LaunchRecorder(copies=self._copies, park_cycles=self._park)
+        _recorder = LaunchRecorder(copies=self._copies, park_cycles=self._park,
+                                   per_copy=self._per_copy)
         return _recorder
 
     def __exit__(self, *exc) -> None:
@@ -589,10 +616,13 @@ def copy_h2d(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) ->
     nbytes = src.numel() * src.element_size()
     if nbytes != dst.numel() * dst.element_size():
         raise ValueError("copy_h2d size mismatch")
-    if _recorder is not None:
-        _recorder._copy_started(stream, nbytes)
+    rec = _recorder
+    if rec is not None:
+        rec._copy_started(stream, nbytes)
     rc = _native.lib().sf_copy_h2d(_ptr(dst), _ptr(src), nbytes, int(stream.cuda_stream))
     _native.check(rc, "sf_copy_h2d")
+    if rec is not None:
+        rec._copy_ended(stream)
 
 
 def stage_record(staging_ptr: int, record_ptr: int, nbytes: int,
@@ -601,10 +631,13 @@ def stage_record(staging_ptr: int, record_ptr: int, nbytes: int,
     staging buffer, from pointers the caller has validated once (the expert
     cache's per-transfer path; ``copy_h2d`` and ``expert_decode`` are the
     checked forms)."""
-    if _recorder is not None:
-        _recorder._copy_started(stream, nbytes)
+    rec = _recorder
+    if rec is not None:
+        rec._copy_started(stream, nbytes)
     rc = _native.lib().sf_copy_h2d(staging_ptr, record_ptr, nbytes, int(stream.cuda_stream))
     _native.check(rc, "sf_copy_h2d")
+    if rec is not None:
+        rec._copy_ended(stream)
 
 
 def decode_staged(staging_ptr: int, nbytes: int, n_values: int, table_c, counts: tuple,

@@ -175,6 +175,32 @@ def test_decode_stats():
     assert d["frac"] == pytest.approx(d["gbs"] / bench.HBM_PEAK_GBS)
 
 
+def test_link_stats_splits_idle_link_time():
+    class _Rec:
+        copy_spans, marks = [], []
+
+    assert bench.link_stats(_Rec(), []) is None
+    rec = _Rec()
+    ms = lambda *xs: [_Ev(x) for x in xs]
+    # Forward 1 (0 .. 1 ms): two overlapping copies, a 50 us gap inside
+    # layer 0, a 150 us gap across layer 1's router (0.5 ms), one more copy.
+    # Forward 2 (2 .. 3 ms): copies run through layer 1's router.
+    rec.copy_spans = [tuple(ms(a, b)) for a, b in
+                      ((0.05, 0.2), (0.1, 0.3), (0.35, 0.45), (0.6, 0.9), (2.1, 2.6),
+                       (2.55, 2.9))]
+    rec.marks = [(0, _Ev(0.0)), (1, _Ev(0.5)), (0, _Ev(2.0)), (1, _Ev(2.5))]
+    steps = [tuple(ms(0.0, 1.0)), tuple(ms(2.0, 3.0))]
+    got = bench.link_stats(rec, steps)
+    assert got["forwards"] == 2 and got["copies"] == 6
+    assert got["boundary_idle_us"]["boundaries"] == 2
+    assert got["boundary_idle_us"]["mean"] == pytest.approx(75.0)
+    assert got["boundary_idle_us"]["median"] == pytest.approx(150.0)
+    want = dict(busy=0.725, one=0.65, two=0.075, boundary=0.075, within=0.025, prologue=0.075,
+                epilogue=0.1)
+    for key, value in want.items():
+        assert got["ms_per_forward"][key] == pytest.approx(value), key
+
+
 @pytest.mark.parametrize("argv,steps", [([], 50), (["--workload", "verify48"], 10),
                                         (["--workload", "cold48"], 10), (["--steps", "7"], 7)])
 def test_bench_step_defaults(monkeypatch, argv, steps):
