@@ -169,6 +169,14 @@ def summarize(fetch_dir: str, write_dir: str, command: str | None = None) -> str
     return "\n".join(lines) + "\n"
 
 
+# Kernel names of libspecfit_amd (K1-K8), listed in the trace summaries.
+LIBRARY_KERNELS = ("router_logits_kernel", "router_select_kernel", "dispatch_kernel",
+                   "gateup_mfma_kernel", "down_mfma_kernel", "gateup_generic_kernel",
+                   "down_generic_kernel", "combine_kernel", "decode_kernel",
+                   "tree_attention_kernel", "tree_attention_mfma_kernel", "rms_norm_kernel",
+                   "qk_norm_rope_kernel", "router_topk_scalar_kernel")
+
+
 def summarize_trace(trace_dir: str, command: str | None = None,
                     title: str = "Qwen3-30B-A3B MoE layer, 64 tree tokens, 24-slot cache",
                     split: bool = True) -> str:
@@ -197,6 +205,18 @@ def summarize_trace(trace_dir: str, command: str | None = None,
         lines.append(f"| `{short[:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                      f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
                      f"{float(r['Percentage']):.1f}% |")
+    own = [r for r in stats if any(k in r["Name"] for k in LIBRARY_KERNELS)]
+    if own:
+        lines += ["", "## Kernels of libspecfit_amd (every instantiation)", "",
+                  "| kernel | calls | avg µs | min µs | max µs | share |",
+                  "|---|---|---|---|---|---|"]
+        for r in own:
+            short = r["Name"].replace("void ", "").replace("(anonymous namespace)::", "")
+            if short.endswith(")"):
+                short = short[:short.rfind("(")]
+            lines.append(f"| `{short[:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                         f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                         f"{float(r['Percentage']):.1f}% |")
     cal = [i for i, r in enumerate(trace) if CALIBRATION_TAG in r["Kernel_Name"]]
     k3 = [(i, r) for i, r in enumerate(trace)
           if "gateup_mfma_kernel" in r["Kernel_Name"] or "down_mfma_kernel" in r["Kernel_Name"]]

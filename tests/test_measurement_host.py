@@ -129,7 +129,13 @@ def test_trace_summary_averages_k3_launches_per_phase(tmp_path):
         w = csv.writer(fh)
         w.writerow(["Name", "Calls", "AverageNs", "MinNs", "MaxNs", "Percentage"])
         w.writerow([_name("gateup", 2), 1, 55000, 55000, 55000, 40.0])
+        w.writerow(["void at::native::elementwise_kernel<128>(int)", 9, 2000, 1000, 3000, 1.0])
+        w.writerow(["void (anonymous namespace)::qk_norm_rope_kernel(unsigned short const*)", 48,
+                    4900, 4500, 5200, 2.0])
     text = pmc.summarize_trace(str(d))
+    library = text.split("## Kernels of libspecfit_amd")[1].split("##")[0]
+    assert "`qk_norm_rope_kernel` | 48 | 4.90 | 4.50 | 5.20 | 2.0% |" in library
+    assert "gateup_mfma_kernel" in library and "elementwise_kernel" not in library
     lines = {l.split("|")[1].strip(): l for l in text.splitlines()
              if l.startswith("| in-step") or l.startswith("| all-resident")}
     table_row = [c.strip() for c in lines["all-resident, slot table"].split("|")[1:-1]]
