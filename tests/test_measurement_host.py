@@ -156,6 +156,30 @@ class _Ev:
         return other.t - self.t
 
 
+def test_trace_summary_without_split_starts_at_the_first_router(tmp_path):
+    d = tmp_path / "trace"
+    d.mkdir()
+    rows, t = [], 0
+    for name, dur in (("void encode_setup_kernel(int)", 50_000),
+                      ("void (anonymous namespace)::router_logits_kernel<4>(int)", 6_000),
+                      ("void (anonymous namespace)::decode_kernel(int)", 10_000),
+                      ("void (anonymous namespace)::decode_kernel(int)", 12_000),
+                      ("void (anonymous namespace)::router_logits_kernel<4>(int)", 4_000)):
+        rows.append({"Kernel_Name": name, "Grid_Size_X": 1, "Start_Timestamp": t,
+                     "End_Timestamp": t + dur})
+        t += dur + 500
+    with open(d / "f_kernel_trace.csv", "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    with open(d / "f_kernel_stats.csv", "w", newline="") as fh:
+        csv.writer(fh).writerow(["Name", "Calls", "AverageNs", "MinNs", "MaxNs", "Percentage"])
+    text = pmc.summarize_trace(str(d), split=False)
+    assert "from the first router launch on" in text and "encode_setup_kernel" not in text
+    assert "| `decode_kernel` | 2 | 11.00 | 10.00 | 12.00 | 68.8% |" in text
+    assert "| `router_logits_kernel<4>` | 2 | 5.00 | 4.00 | 6.00 | 31.2% |" in text
+
+
 def test_bench_helpers():
     assert bench._union_length([(0, 2), (1, 3), (5, 6)]) == 4
     assert bench._union_length([]) == 0
