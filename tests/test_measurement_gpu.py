@@ -89,3 +89,26 @@ def test_bench_48_layer_forward_under_the_prefetch_scheduler(device, workload, e
         assert per["unused_prediction_copies"] == 0
     else:
         assert per["predicted_experts"] == 0 and per["prediction_copies"] == 0
+
+
+def test_bench_link_breakdown_of_the_48_layer_forward(device):
+    """--record copies on the cold forward, shrunk to 2 layers: the link
+    block counts every copy of the recorded pass and one boundary per
+    forward, and its times add up."""
+    cmd = [sys.executable, "-u", os.path.join(ROOT, "bench.py"), "--workload", "cold48",
+           "--layers", "2", "--tree-nodes", "8", "--context", "64", "--expert-sets", "2",
+           "--steps", "2", "--warmup", "1", "--record", "copies", "--cpu-seconds", "0"]
+    print("bench link run:", " ".join(cmd[2:]), flush=True)
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=110, cwd=ROOT)
+    assert out.returncode == 0, out.stderr[-3000:]
+    d = json.loads([line for line in out.stdout.splitlines() if line.strip()][-1])
+    link = d["link"]
+    assert link["forwards"] == 2
+    assert link["copies"] == d["h2d"]["transfers"] > 0
+    assert link["boundary_idle_us"]["boundaries"] == 2  # layer 1's router, per forward
+    ms = link["ms_per_forward"]
+    assert all(v >= 0 for v in ms.values()) and ms["busy"] > 0
+    assert ms["busy"] == pytest.approx(ms["one"] + ms["two"], rel=1e-6)
+    device_ms = d["device_ms_per_step"]["median"]
+    spent = ms["busy"] + ms["boundary"] + ms["within"] + ms["prologue"] + ms["epilogue"]
+    assert spent == pytest.approx(device_ms, rel=0.5)
