@@ -492,8 +492,18 @@ class Qwen3ExpertPrefetch:
         self._routed_layer = layer
         self._remaining = remaining = {e: plan.key(e) for e in sorted(actual)}
         self._ready_ids = set()
+        cache = plan.cache
+        resident, inflight, sources = cache._resident, cache._inflight, cache._sources
+        holds = self._holds
+        closed = cache._closed
         for e, key in remaining.items():
-            hold = self._holds.get(key) or self._hold(key, _RESIDENT_ONLY)
+            hold = holds.get(key)
+            if hold is None and (closed or key in resident or key in inflight
+                                 or key not in sources):
+                # Only these keys can be held (or make the cache raise): the
+                # resident-only lookup of any other key returns nothing and
+                # touches nothing, so it is skipped.
+                hold = self._hold(key, _RESIDENT_ONLY)
             if hold is None:
                 stats.missing_at_router += 1
             elif hold.ready:
@@ -501,7 +511,7 @@ class Qwen3ExpertPrefetch:
                 self._ready_ids.add(e)
             else:
                 stats.inflight_at_router += 1
-        plan.requests = deque(k for k in remaining.values() if k not in self._holds)
+        plan.requests = deque(k for k in remaining.values() if k not in holds)
         return plan
 
     def _oldest_in_flight(self) -> _Hold | None:
