@@ -231,6 +231,30 @@ def test_link_stats_splits_idle_link_time():
         assert got["ms_per_forward"][key] == pytest.approx(value), key
 
 
+def test_link_stats_forward_without_copies_and_copies_through_every_boundary():
+    """A forward whose experts were all resident (no copies) counts as a
+    forward but contributes no link time; copies that run through every
+    router give zero boundary idle."""
+    class _Rec:
+        copy_spans, marks = [], []
+
+    rec = _Rec()
+    rec.copy_spans = [(_Ev(2.1), _Ev(2.6)), (_Ev(2.5), _Ev(2.95))]
+    rec.marks = [(0, _Ev(0.0)), (1, _Ev(0.5)), (0, _Ev(2.0)), (1, _Ev(2.4)), (2, _Ev(2.55))]
+    steps = [(_Ev(0.0), _Ev(1.0)), (_Ev(2.0), _Ev(3.0))]
+    got = bench.link_stats(rec, steps)
+    assert got["forwards"] == 2 and got["copies"] == 2
+    b = got["boundary_idle_us"]
+    # Forward 2: layer 1's router (2.4 ms) falls before the first copy, so
+    # no gap holds it; layer 2's (2.55 ms) falls inside the copies.
+    assert b["boundaries"] == 2 and b["median"] == 0.0 and b["mean"] == 0.0
+    ms = got["ms_per_forward"]
+    assert ms["busy"] == pytest.approx(0.85 / 2)
+    assert ms["two"] == pytest.approx(0.1 / 2) and ms["one"] == pytest.approx(0.75 / 2)
+    assert ms["within"] == 0.0 and ms["boundary"] == 0.0
+    assert ms["prologue"] == pytest.approx(0.1 / 2) and ms["epilogue"] == pytest.approx(0.05 / 2)
+
+
 @pytest.mark.parametrize("argv,steps", [([], 50), (["--workload", "verify48"], 10),
                                         (["--workload", "cold48"], 10), (["--steps", "7"], 7)])
 def test_bench_step_defaults(monkeypatch, argv, steps):
