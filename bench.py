@@ -35,8 +35,8 @@ measurement of the same workload whose misses copy the raw bf16 expert bytes
 as the reference does (``raw_transfer``), and shorter runs of the other
 benchmark configurations (``other_configs``: 16 tokens all resident, the
 1-128 token sweep, the 48-layer verification forward and the cold 128-token
-forward), each exactly as its ``--workload`` run measures it, with fewer
-steps.
+forward, the last two also under the reference's ready_demand executor),
+each exactly as its ``--workload`` run measures it, with fewer steps.
 
 Prints ONE JSON line on stdout; diagnostics go to stderr.
 """
@@ -115,7 +115,8 @@ def parse_args(argv=None):
                         "raw transfers (reported as raw_transfer)")
     p.add_argument("--no-other-configs", dest="other_configs", action="store_false",
                    help="single-layer workload: skip the shorter runs of the other "
-                        "configurations (other_configs: resident16, sweep, verify48, cold48)")
+                        "configurations (other_configs: resident16, sweep, verify48, cold48, "
+                        "and the last two under the ready_demand executor)")
     p.add_argument("--config-steps", type=int, default=20,
                    help="steps per pass of the resident16 and sweep runs in other_configs")
     p.add_argument("--record", choices=("full", "k3", "none", "copies"), default="full",
@@ -688,7 +689,8 @@ def other_configs(args) -> dict:
     """The other benchmark configurations, each in a shorter run of its own
     (fewer steps; the same code path as ``--workload``):
     16 tokens all resident; the 1-128 token sweep; the 48-layer
-    verification forward and the cold 128-token forward."""
+    verification forward and the cold 128-token forward, each with the
+    per-layer executor and with the reference's ready_demand executor."""
     steps, tr = str(args.config_steps), ["--transfer", args.transfer]
     # The 48-layer runs take the forward's shape options of this run.
     shape = ["--layers", str(args.layers), "--context", str(args.context),
@@ -710,19 +712,27 @@ def other_configs(args) -> dict:
     def verify_pick(d):
         return {"value": d["value"], "unit": d["unit"], "ms_per_step": d["ms_per_step"],
                 "workload": d["config"]["workload"], "transfer": d["config"]["transfer"],
+                "executor": d["config"]["executor"],
                 "per_layer_tokens_per_s": d["per_layer_tokens_per_s"],
                 "misses_per_layer": d["cache"]["misses_per_layer"]}
+
+    verify_args = ["--workload", "verify48", "--steps", "5", "--warmup", "2", "--record", "none",
+                   "--tree-nodes", str(args.tree_nodes), *shape, *tr]
+    cold_args = ["--workload", "cold48", "--steps", "5", "--warmup", "2", "--record", "none",
+                 *shape, *tr]
+    # The same forwards under the reference's measured decode executor (the
+    # prefetch scheduler with no predictions, lookahead 0, two credits).
+    rd = ["--executor", "ready_demand"]
 
     return {
         "resident16": _config_run(["--workload", "resident16", "--steps", steps, "--warmup", "5",
                                    "--cpu-seconds", "2", "--record", "k3"], layer_pick),
         "sweep": _config_run(["--workload", "sweep", "--steps", steps, "--warmup", "5",
                               "--record", "k3", *tr], sweep_pick),
-        "verify48": _config_run(["--workload", "verify48", "--steps", "5", "--warmup", "2",
-                                 "--record", "none", "--tree-nodes", str(args.tree_nodes),
-                                 *shape, *tr], verify_pick),
-        "cold48": _config_run(["--workload", "cold48", "--steps", "5", "--warmup", "2",
-                               "--record", "none", *shape, *tr], verify_pick),
+        "verify48": _config_run(verify_args, verify_pick),
+        "cold48": _config_run(cold_args, verify_pick),
+        "verify48_ready_demand": _config_run(verify_args + rd, verify_pick),
+        "cold48_ready_demand": _config_run(cold_args + rd, verify_pick),
     }
 
 

@@ -52,13 +52,15 @@ def test_bench_prints_one_contract_line(device):
     assert 0 < raw["k3_in_step_gbs"] < 8000.0
     # the other configurations, each in a short run of its own
     other = d["other_configs"]
-    assert set(other) == {"resident16", "sweep", "verify48", "cold48"}
+    assert set(other) == {"resident16", "sweep", "verify48", "cold48", "verify48_ready_demand",
+                          "cold48_ready_demand"}
     assert all("error" not in v for v in other.values()), other
     assert other["resident16"]["value"] > 0 and 0 < other["resident16"]["k3_frac"] < 1
     assert [p["tokens"] for p in other["sweep"]["points"]] == [1, 8, 32, 64, 128]
     assert all(p["tokens_per_s"] > 0 for p in other["sweep"]["points"])
-    for name in ("verify48", "cold48"):
+    for name in ("verify48", "cold48", "verify48_ready_demand", "cold48_ready_demand"):
         assert other[name]["value"] > 0 and "2 layers" in other[name]["workload"]
+        assert other[name]["executor"] == ("ready_demand" if "ready" in name else "layer")
 
 
 
