@@ -490,19 +490,25 @@ class Qwen3ExpertPrefetch:
         stats.unused_prediction_copies = len(plan.prediction_copies - actual)
         self._advance()
         self._routed_layer = layer
-        self._remaining = remaining = {e: plan.key(e) for e in sorted(actual)}
+        keys = plan.keys
+        get = keys.get
+        self._remaining = remaining = {e: get(e) or ExpertKey(layer, e) for e in sorted(actual)}
         self._ready_ids = set()
         cache = plan.cache
-        resident, inflight, sources = cache._resident, cache._inflight, cache._sources
-        holds = self._holds
-        closed = cache._closed
+        # Expert ids (int hashing) rather than keys from here on.
+        held = {k.expert_id: h for k, h in self._holds.items() if k.layer_id == layer}
+        if cache._closed:
+            lookup = actual  # the cache raises for any of them
+        else:
+            # Only these experts can be held (or make the cache raise: ids
+            # the layer's sources lack); the resident-only lookup of any
+            # other returns nothing and touches nothing, so it is skipped.
+            lookup = {k.expert_id for m in (cache._resident, cache._inflight) for k in m
+                      if type(k) is ExpertKey and k.layer_id == layer}
+            lookup.update(e for e in actual if e not in keys)
         for e, key in remaining.items():
-            hold = holds.get(key)
-            if hold is None and (closed or key in resident or key in inflight
-                                 or key not in sources):
-                # Only these keys can be held (or make the cache raise): the
-                # resident-only lookup of any other key returns nothing and
-                # touches nothing, so it is skipped.
+            hold = held.get(e)
+            if hold is None and e in lookup:
                 hold = self._hold(key, _RESIDENT_ONLY)
             if hold is None:
                 stats.missing_at_router += 1
@@ -511,7 +517,8 @@ class Qwen3ExpertPrefetch:
                 self._ready_ids.add(e)
             else:
                 stats.inflight_at_router += 1
-        plan.requests = deque(k for k in remaining.values() if k not in holds)
+        held = {k.expert_id for k in self._holds if k.layer_id == layer}
+        plan.requests = deque(k for e, k in remaining.items() if e not in held)
         return plan
 
     def _oldest_in_flight(self) -> _Hold | None:
