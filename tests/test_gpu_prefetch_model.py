@@ -449,6 +449,9 @@ def test_loader_can_keep_the_eager_dense_modules(device):
                 # 2 layers x (input, post-attention, q, k) + the final norm
                 assert (eager_norms, hip_norms) == ((0, 9) if hip else (9, 0)), hip
                 assert eager_attn == (0 if hip else 2), hip
+                if hip:  # one GEMM over the fused [q; k; v] weights in every layer
+                    assert all(layer.self_attn._fused_projection()
+                               for layer in loaded.model.model.layers)
                 with torch.inference_mode():
                     got = loaded.model(ids.to(device), use_cache=False).logits.float().cpu()
                 torch.testing.assert_close(got, hf, rtol=3e-2, atol=3e-2)
